@@ -1,0 +1,228 @@
+"""Benchmark of the TriAttention KV-compression step on one MI355X.
+
+A step is one batched pass of the hot path over the whole synthetic batch:
+phase table -> paged-K scoring of the sampled layers -> head statistics ->
+aggregate -> keep-set selection -> K/V compaction of every layer -> block-table
+rewrite.  Inputs are resident in HBM before timing starts.
+
+Default workload: Qwen2.5-14B-shaped cache (48 layers, 40 query / 8 KV heads,
+head_dim 128, bf16), 16 sequences x 16384 tokens in randomly permuted
+128-token pages, budget 4096, recent window 128, score-layer stride 8.
+
+Prints one JSON line: tokens/s (value), the compaction kernel's achieved HBM
+bandwidth against MI355X peak (roofline), per-stage times, and the CPU
+baseline (the oracle's torch restatement of the reference path, timed on a
+bounded one-sequence sample on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "vllm-ascend-kvcompress-hust_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--config", type=int, default=2, help="workload configuration 1-5")
+    p.add_argument("--layers", type=int, default=None, help="override the materialised layer count")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-repeats", type=int, default=3)
+    return p.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_stages(pipeline, batch, steps: int, warmup: int):
+    import torch
+
+    for _ in range(warmup):
+        pipeline.step(batch)
+    torch.cuda.synchronize()
+    names = ("score", "aggregate", "select", "compact", "rewrite")
+    events = {n: [] for n in names}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        pipeline.validate(batch)
+        marks[0].record()
+        pipeline.score(batch)
+        marks[1].record()
+        pipeline.aggregate(batch)
+        marks[2].record()
+        pipeline.select(batch)
+        marks[3].record()
+        pipeline.compact(batch)
+        marks[4].record()
+        pipeline.rewrite(batch)
+        marks[5].record()
+        for i, n in enumerate(names):
+            events[n].append((marks[i], marks[i + 1]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    stage_ms = {n: statistics.mean(a.elapsed_time(b) for a, b in pairs) for n, pairs in events.items()}
+    return wall, stage_ms
+
+
+def cpu_baseline(cache, spec, repeats: int) -> dict:
+    """Time the oracle (torch CPU restatement of the reference path) on one
+    sequence: score the sampled layers, select, materialise every layer."""
+    import torch
+
+    from oracle import triattention_ref as ref
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    b = 0
+    n = spec.seq_lens[b]
+    src = cache.source_tables[b]
+    dst = cache.destination_tables[b] if cache.destination_tables is not None else src[: -(-spec.budget // 128)]
+    pages = torch.cat([src, dst]).unique()
+    remap = {int(p): i for i, p in enumerate(pages.tolist())}
+    h_src = torch.tensor([remap[int(p)] for p in src.tolist()])
+    h_dst = torch.tensor([remap[int(p)] for p in dst.tolist()])
+    k_host = [k[pages].cpu() for k in cache.k_caches]
+    v_host = [v[pages].cpu() for v in cache.v_caches]
+    stats = cache.calibration.to_device(spec.model_shape(), torch.device("cpu"))
+    layer_stats = [
+        ref.LayerStats(s.q_mean_real, s.q_mean_imag, s.q_abs_mean, s.freq_scale_sq, s.omega, s.rope_style, s.rotary_dim, s.q_pass_mean)
+        for s in (stats[layer] for layer in spec.scoring_layers)
+    ]
+    cfg = ref.MethodConfig(
+        budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
+        score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
+    )
+    offsets = ref.build_geometric_offsets(spec.max_model_len)
+
+    def one() -> float:
+        t = time.perf_counter()
+        out = ref.method_select([k_host[l] for l in spec.scoring_layers], layer_stats, h_src, n, cache.round_starts[b], offsets, cfg)
+        ref.method_compress(k_host, v_host, h_src, h_dst, out["keep"], spec.budget)
+        return time.perf_counter() - t
+
+    one()  # warm-up
+    times = [one() for _ in range(repeats)]
+    med = statistics.median(times)
+    return {
+        "value": round(n / med, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"1 of {len(spec.seq_lens)} sequences ({n} tokens): score {len(spec.scoring_layers)} layers "
+            f"(chunk 8192), select, materialise {spec.n_layers} layers; median of {repeats} after 1 warm-up; "
+            f"{med:.2f} s per sequence; host CPU {cpu_model()}"
+        ),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on exactly one GPU: the compression step has no cross-GPU work "
+            f"(sequences shard across GPUs with no exchange); --gpus {args.gpus} is not supported",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    from kvcompress_mi355x import workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    overrides = {} if args.layers is None else {"n_layers": args.layers}
+    spec = workloads.config_spec(args.config, **overrides)
+    device = torch.device("cuda:0")
+    cache = workloads.build_synthetic_cache(spec, device, seed=0)
+    pipeline, batch = workloads.build_pipeline(cache)
+    torch.cuda.synchronize()
+
+    wall, stage_ms = time_stages(pipeline, batch, args.steps, args.warmup)
+    ms_per_step = 1000.0 * wall / args.steps
+    tokens = spec.total_tokens
+    value = tokens / (wall / args.steps)
+    algo = spec.algorithmic_bytes()
+    compact_gbs = algo["compact"] / (stage_ms["compact"] / 1000.0) / 1e9
+    total_gbs = algo["total"] / (ms_per_step / 1000.0) / 1e9
+    score_gbs = algo["score"] / (stage_ms["score"] / 1000.0) / 1e9
+
+    traffic = None
+    traffic_file = REPO / "profiles" / f"compact_traffic_config{args.config}.json"
+    if traffic_file.is_file() and args.layers is None:
+        traffic = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+
+    result = {
+        "metric": "KV tokens scored+compacted/sec at 1 GPU; achieved HBM GB/s as % of peak",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if spec.dtype == torch.bfloat16 else "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": spec.name,
+            "layers": spec.n_layers,
+            "scoring_layers": len(spec.scoring_layers),
+            "n_seq": len(spec.seq_lens),
+            "tokens": tokens,
+            "budget": spec.budget,
+            "recent": spec.recent,
+            "policy": spec.policy,
+            "heads": f"{spec.num_attention_heads}q/{spec.num_kv_heads}kv",
+            "head_dim": spec.head_dim,
+            "compaction": "in-place" if spec.inplace else "private destinations",
+        },
+        "roofline": {
+            "kernel": "kvc_compact",
+            "bound": "hbm",
+            "achieved": round(compact_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(compact_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": algo["compact"],
+        },
+        "step_hbm": {
+            "algorithmic_bytes": algo["total"],
+            "achieved_gbs": round(total_gbs, 1),
+            "frac": round(total_gbs / HBM_PEAK_GBS, 4),
+        },
+        "stages_ms": {k: round(v, 4) for k, v in stage_ms.items()},
+        "score_gbs": round(score_gbs, 1),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cache, spec, args.cpu_repeats)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

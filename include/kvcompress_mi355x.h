@@ -1,0 +1,215 @@
+/*
+ * kvcompress_mi355x.h -- C ABI of the MI355X TriAttention KV-compression path.
+ *
+ * Path: paged-K trigonometric scoring -> per-head normalisation and
+ * cross-layer aggregation -> per-sequence keep-set selection -> K/V
+ * compaction with block-table rewrite and page release.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers unless the parameter name ends in
+ *     "_host".  Nothing is allocated and nothing is freed; scratch memory is
+ *     passed in by the caller (sizes come from the *_workspace_bytes queries).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *     never synchronised.
+ *   - Return value: 0 on success, KVC_EINVAL for rejected arguments, or a
+ *     positive hipError_t from the launch.  kvc_last_error() returns the
+ *     message of the last failure on the calling thread.
+ *   - Caches use the reference layout [num_pages][128][kv_heads][head_dim]
+ *     (bf16 or fp16) with contiguous inner dimensions and a page stride
+ *     >= 128*kv_heads*head_dim elements (pkg/provider.py:1201-1230).
+ *     Per-layer caches are named by a device table of base addresses.
+ *   - Token blocks are 128 tokens (pkg/config.py:18, ASCEND_BLOCK_SIZE).
+ *   - Block tables are int64 (source_block_ids_device, pkg/methods/base.py:74).
+ *     A batch of sequences uses ragged tables: sequence b owns
+ *     block_ids[block_offsets[b] .. block_offsets[b+1]).
+ *
+ * Citations are to the reference repository vLLM-HUST/vllm-ascend-kvcompress-hust
+ * v0.10.0 with tri/ = src/vllm_ascend_kvcompress/methods/triattention/ and
+ * pkg/ = src/vllm_ascend_kvcompress/.
+ */
+#ifndef KVCOMPRESS_MI355X_H
+#define KVCOMPRESS_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* kvc_stream_t; /* hipStream_t */
+
+#define KVC_ABI_VERSION 1
+#define KVC_BLOCK_SIZE 128
+#define KVC_EINVAL (-22)
+
+enum kvc_dtype { KVC_DTYPE_BF16 = 0, KVC_DTYPE_FP16 = 1 };
+enum kvc_rope_style { KVC_ROPE_HALF = 0, KVC_ROPE_INTERLEAVED = 1 };
+enum kvc_policy { KVC_POLICY_GLOBAL = 0, KVC_POLICY_V3 = 1 };
+enum kvc_layer_aggregation { KVC_LAYER_MEAN = 0, KVC_LAYER_MAX = 1 };
+
+/* Flags of kvc_aggregate. */
+#define KVC_AGG_ACCUMULATE 1u /* combine with the existing aggregate instead of overwriting it */
+#define KVC_AGG_FINALIZE 2u   /* divide by the layer count (mean mode) and sanitise NaN/inf */
+#define KVC_AGG_RSQRT 4u      /* (s-mean)*rsqrt(max(var,1e-6)) instead of (s-mean)/sqrt(max(var,1e-6)) */
+
+/* ABI version and last error message of the calling thread. No counterpart in
+ * the reference (it is a pure-Python plugin). */
+int kvc_abi_version(void);
+const char* kvc_last_error(void);
+
+/* ---------------------------------------------------------------- phases -- */
+
+/* Mean future-position phase coefficients, evaluated directly:
+ *   phase_cos[b][l][f] = mean_o cos((offsets[o] + round_starts[b]) * omega[l][f])
+ *   phase_sin[b][l][f] = mean_o sin((offsets[o] + round_starts[b]) * omega[l][f])
+ * Replaces the torch path's phase evaluation inside score_post_rope_keys
+ * (tri/scoring.py:77-80) for every sequence and scoring layer at once. */
+int kvc_mean_phases(kvc_stream_t stream, int n_seq, int n_layers, int n_freq,
+                    const int64_t* round_starts, const float* offsets, int n_offsets,
+                    const float* omega, float* phase_cos, float* phase_sin);
+
+/* Angle-addition form of the reference's device path:
+ *   phase_cos = cos(rs*omega)*offset_cos_mean - sin(rs*omega)*offset_sin_mean
+ *   phase_sin = sin(rs*omega)*offset_cos_mean + cos(rs*omega)*offset_sin_mean
+ * Replaces prepare_mean_phase_coefficients (tri/kernels.py:50-122). */
+int kvc_shift_mean_phases(kvc_stream_t stream, int n_values, int64_t round_start,
+                          const float* omega, const float* offset_cos_mean,
+                          const float* offset_sin_mean, float* phase_cos, float* phase_sin);
+
+/* --------------------------------------------------------------- scoring -- */
+
+/* Bytes of scratch kvc_score_paged needs for this shape. */
+size_t kvc_score_workspace_bytes(int n_layers, int kv_heads, int head_dim, int rotary_dim,
+                                 int qpk, int n_seq, int max_seq_len);
+
+/* Raw TriAttention scores of every cached token against the calibrated query
+ * centres (tri/scoring.py:23-120, device form tri/kernels.py:125-317):
+ *   score[l][b][t][h*qpk+g] = sum_f a*((qr*kr+qi*ki)*c_f - (qi*kr-qr*ki)*s_f)
+ *                           + sum_f a*extra*|k_f| + sum_p q_pass*k_pass
+ * for the n_layers scoring layers, all sequences of the batch, reading K once
+ * per KV head through the block tables (token t of sequence b lives in page
+ * block_ids[block_offsets[b] + t/128], row t%128).
+ *
+ * Calibration inputs are per scoring layer, grouped by KV head, float32:
+ *   q_real, q_imag, freq_scale (= sqrt(freq_scale_sq)), extra_coef
+ *   (= q_abs_mean - sqrt(q_real^2+q_imag^2+1e-8)): [n_layers][kv_heads][qpk][F]
+ *   q_pass: [n_layers][kv_heads][qpk][head_dim-rotary_dim], NULL when full RoPE.
+ * phase_cos/phase_sin: [n_seq][n_layers][F] with sequence stride
+ * phase_seq_stride elements (0 = one table shared by all sequences).
+ * Output element (l, b, t, q) is written at
+ *   raw[l*raw_layer_stride + (token_offsets[b]+t)*raw_token_stride + q*raw_head_stride].
+ * The workspace also receives per-tile float64 partial sums used by
+ * kvc_head_stats; it must stay untouched until that call. */
+int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers, const uint64_t* k_layer_ptrs,
+                    int64_t num_pages, int64_t page_stride, int kv_heads, int head_dim,
+                    int rotary_dim, int qpk, int rope_style, int n_seq, int max_seq_len,
+                    const int32_t* seq_lens, const int64_t* token_offsets,
+                    const int64_t* block_offsets, const int64_t* block_ids, const float* q_real,
+                    const float* q_imag, const float* freq_scale, const float* extra_coef,
+                    const float* q_pass, const float* phase_cos, const float* phase_sin,
+                    int64_t phase_seq_stride, float* raw, int64_t raw_layer_stride,
+                    int64_t raw_token_stride, int64_t raw_head_stride, void* workspace,
+                    size_t workspace_bytes);
+
+/* Population mean and variance of every query head's raw scores over the
+ * sequence's tokens, from the partial sums kvc_score_paged left in the
+ * workspace (torch.var_mean(raw, dim=-1, correction=0), tri/method.py:379-381,423).
+ * mean/var: float32 [n_layers][n_seq][kv_heads*qpk]. Same shape arguments as
+ * the kvc_score_paged call that filled the workspace. */
+int kvc_head_stats(kvc_stream_t stream, int n_layers, int kv_heads, int head_dim, int rotary_dim,
+                   int qpk, int n_seq, int max_seq_len, const int32_t* seq_lens,
+                   const void* workspace, size_t workspace_bytes, float* mean, float* var);
+
+/* Normalise, take the max over query heads and combine across layers
+ * (normalize_head_scores + _aggregate_torch, tri/scoring.py:123-128,
+ * tri/method.py:477-503; device form tri/kernels.py:365-437; layer mean and
+ * nan_to_num tri/method.py:463-467):
+ *   z = (raw - mean) / sqrt(max(var, 1e-6))       per (layer, seq, head, token)
+ *   layer_score = max_h z                          (NaN-propagating)
+ *   agg = layer_score[0] (+ or max) layer_score[1] ... in layer order
+ * flags: KVC_AGG_ACCUMULATE combines layer 0 with the existing agg contents;
+ * KVC_AGG_FINALIZE divides by n_layers (mean mode) and maps NaN->-inf,
+ * +inf->1e30; KVC_AGG_RSQRT uses the reference device kernel's rsqrt form.
+ * mean/var addressed as [l*stats_layer_stride + b*stats_seq_stride + h].
+ * agg element (b, t) lives at agg[token_offsets[b] + t]. */
+int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int n_seq, int max_seq_len,
+                  const int32_t* seq_lens, const int64_t* token_offsets, const float* raw,
+                  int64_t raw_layer_stride, int64_t raw_token_stride, int64_t raw_head_stride,
+                  const float* mean, const float* var, int64_t stats_layer_stride,
+                  int64_t stats_seq_stride, int layer_aggregation, unsigned flags, float* agg);
+
+/* ------------------------------------------------------------- selection -- */
+
+/* Sorted keep indices of every sequence (select_keep_indices,
+ * tri/selection.py:108-196): protected prefix/recent windows are always kept;
+ * policy GLOBAL keeps the top (budget - protected) scores of the middle;
+ * policy V3 splits the middle into `segments` ranges with proportional
+ * integer eviction quotas (tri/selection.py:165-189) and keeps each range's
+ * top scores.  Ties at the selection threshold go to the lowest index.
+ * scores: agg layout of kvc_aggregate.  keep: int64 [n_seq][keep_stride],
+ * the first `budget` entries of each row written in ascending order.
+ * The caller has validated budget/windows against every seq_len as the
+ * reference does (tri/selection.py:123-133). */
+int kvc_select_keep(kvc_stream_t stream, int n_seq, int max_seq_len, const int32_t* seq_lens,
+                    const int64_t* token_offsets, const float* scores, int budget,
+                    int protected_prefix, int protected_recent, int segments, int policy,
+                    int64_t* keep, int64_t keep_stride);
+
+/* ------------------------------------------------------------ compaction -- */
+
+/* Move the kept K and V rows of every layer into their destinations
+ * (token_slots + materialize_token_slots over all layers,
+ * tri/method.py:272-288, tri/cache.py:9-15,100-112):
+ *   row keep[b][i] of the source table  ->  row i of the destination table
+ * for i < budget.  dst_block_ids == NULL selects in-place mode: destinations
+ * are the front pages of the source table (dst page i/128 = source page i/128);
+ * the kernel orders every read of a row before the write that overwrites it.
+ * Otherwise destination pages must be private (disjoint from the source pages).
+ * row_elems = kv_heads*head_dim; elem_bytes = 2. */
+int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_layer_ptrs,
+                const uint64_t* v_layer_ptrs, int64_t num_pages, int64_t page_stride,
+                int64_t row_elems, int elem_bytes, int n_seq, const int32_t* seq_lens,
+                const int64_t* src_block_offsets, const int64_t* src_block_ids,
+                const int64_t* dst_block_offsets, const int64_t* dst_block_ids,
+                const int64_t* keep, int64_t keep_stride, int budget);
+
+/* New block table and released pages after compaction (PendingCompression and
+ * the scheduler commit, pkg/provider.py:596-601, pkg/stateful.py:327-338):
+ *   new_tables[b][j] = destination page j (j < ceil(budget/128))
+ *   freed pages of b = reversed(source pages not reused), written at
+ *   freed_ids[freed_offsets[b] ...]; in-place mode reuses the first
+ *   ceil(budget/128) source pages, private mode releases every source page.
+ * freed_offsets is computed by the caller (it knows the table lengths). */
+int kvc_rewrite_block_tables(kvc_stream_t stream, int n_seq, int budget,
+                             const int64_t* src_block_offsets, const int64_t* src_block_ids,
+                             const int64_t* dst_block_offsets, const int64_t* dst_block_ids,
+                             int64_t* new_tables, const int64_t* freed_offsets,
+                             int64_t* freed_ids);
+
+/* ------------------------------------------------------- slot utilities -- */
+
+/* Logical token -> flat physical slot: block_ids[t/block_size]*block_size + t%block_size
+ * (token_slots, tri/cache.py:9-15). Out-of-table tokens yield -1. */
+int kvc_token_slots(kvc_stream_t stream, const int64_t* block_ids, int64_t n_blocks,
+                    const int64_t* token_indices, int64_t n_tokens, int block_size,
+                    int64_t* slots);
+
+/* Scheduler page id -> consecutive 128-token kernel block ids:
+ * out[i*k + j] = ids[i]*k + j (_expand_scheduler_block_ids, pkg/provider.py:1273-1287). */
+int kvc_expand_block_ids(kvc_stream_t stream, const int64_t* ids, int64_t n_ids, int k,
+                         int64_t* out);
+
+/* Slot-addressed gather -> workspace -> scatter of K and V rows, safe for any
+ * overlap between source and destination slots (materialize_token_slots,
+ * tri/cache.py:100-112).  k_ws/v_ws hold n_slots*row_bytes bytes each. */
+int kvc_materialize_slots(kvc_stream_t stream, void* k_cache, void* v_cache, int64_t num_pages,
+                          int64_t page_stride, int64_t row_elems, int elem_bytes,
+                          const int64_t* src_slots, const int64_t* dst_slots, int64_t n_slots,
+                          void* k_ws, void* v_ws);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVCOMPRESS_MI355X_H */

@@ -1,0 +1,28 @@
+"""CPU oracle of the TriAttention compression path -- TEST INFRASTRUCTURE ONLY.
+
+Nothing in the product imports this package.  It is used by tests/, by
+__graft_entry__.smoke() as the checker, and by bench.py's cpu_baseline leg as
+the timed CPU baseline ("port" kind).
+
+Modules
+  triattention_ref  torch-CPU restatement of the reference's own torch path
+                    (tri/scoring.py, tri/method.py fallback branch,
+                    tri/selection.py, tri/cache.py), same ops in the same order.
+  brute             float64 brute force (plain loops / numpy) used to pin the
+                    restatement on small inputs, and the deterministic
+                    (score desc, index asc) selection rule.
+
+Parity pins (how each oracle function is checked, see tests/test_oracle_*.py):
+  build_geometric_offsets   closed form 2^k <= max
+  score_post_rope_keys      reference KATs (tests/test_scoring.py:53-133: slow
+                            per-offset reference, scale 4.0, partial-RoPE
+                            [2,-5]); float64 brute force; omega=0 closed form
+  normalize/aggregate       closed form of tests/test_selection.py:271-280;
+                            float64 brute force
+  select_keep_indices       reference KATs ([0,1,4,5], v3 evicts {2,5,8,11},
+                            uneven quota count); brute-force sort; batched-v3
+                            equivalence (tests/test_selection.py:94-125)
+  token_slots/materialize   reference KATs ([8,11,0,3], overlapping write,
+                            padded page stride: tests/test_cache.py:15-94)
+  block-table rewrite       scheduler commit semantics (pkg/stateful.py:327-338)
+"""

@@ -1,0 +1,355 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (needs a GPU)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_agg_close, assert_scores_close
+from oracle import brute
+from oracle import triattention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _kvc():
+    from kvcompress_mi355x.methods.triattention import cache, kernels, selection
+
+    return kernels, selection, cache
+
+
+def _random_stats(g, kv, qpk, freq, pass_dim, rotary, theta=1e6, style="half"):
+    qr = torch.randn(kv, qpk, freq, generator=g)
+    qi = torch.randn(kv, qpk, freq, generator=g)
+    qa = torch.sqrt(qr.square() + qi.square()) + torch.rand(kv, qpk, freq, generator=g)
+    fs = 0.5 + torch.rand(kv, qpk, freq, generator=g)
+    omega = 1.0 / (theta ** (torch.arange(0, rotary, 2, dtype=torch.float32) / rotary))
+    qp = torch.randn(kv, qpk, pass_dim, generator=g) if pass_dim else None
+    return ref.LayerStats(qr, qi, qa, fs, omega, style, rotary, qp)
+
+
+@pytest.mark.parametrize("round_start", [300, 16384, 131072])
+def test_mean_phase_table_matches_torch(hip_device, round_start: int) -> None:
+    kernels, _, _ = _kvc()
+    offsets = ref.build_geometric_offsets(32768)
+    omega = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    omega2 = torch.stack([omega, omega * 0.5])
+    rs = torch.tensor([round_start, round_start + 1], dtype=torch.int64)
+    cos, sin = kernels.mean_phase_table(rs.to(hip_device), offsets.to(hip_device), omega2.to(hip_device))
+    for b in range(2):
+        for layer in range(2):
+            phases = (offsets.unsqueeze(1) + float(rs[b])) * omega2[layer].unsqueeze(0)
+            torch.testing.assert_close(cos[b, layer].cpu(), torch.cos(phases).mean(0), rtol=0, atol=2e-6)
+            torch.testing.assert_close(sin[b, layer].cpu(), torch.sin(phases).mean(0), rtol=0, atol=2e-6)
+
+
+def test_shift_phase_coefficients_formula(hip_device) -> None:
+    kernels, _, _ = _kvc()
+    omega = torch.tensor([[1.0, 0.1, 0.01, 0.001]] * 3)
+    offsets = torch.tensor([1.0, 2.0, 4.0])
+    oc = torch.cos(offsets.unsqueeze(1) * omega[0]).mean(0).expand(3, -1).contiguous()
+    os_ = torch.sin(offsets.unsqueeze(1) * omega[0]).mean(0).expand(3, -1).contiguous()
+    pc = torch.empty(3, 4, device=hip_device)
+    ps = torch.empty_like(pc)
+    assert kernels.prepare_mean_phase_coefficients(omega.to(hip_device), oc.to(hip_device), os_.to(hip_device), 300, pc, ps)
+    rc, rsn = torch.cos(300 * omega.double()), torch.sin(300 * omega.double())
+    torch.testing.assert_close(pc.cpu().double(), rc * oc.double() - rsn * os_.double(), rtol=0, atol=1e-6)
+    torch.testing.assert_close(ps.cpu().double(), rsn * oc.double() + rc * os_.double(), rtol=0, atol=1e-6)
+    # The angle-addition table agrees with direct evaluation within the
+    # reference smoke tolerance (tests/run_npu_kernel_smoke.py:136-138).
+    direct = torch.cos((offsets.unsqueeze(1) + 300.0) * omega[0]).mean(0)
+    torch.testing.assert_close(pc[0].cpu(), direct, rtol=2e-3, atol=2e-3)
+
+
+SCORE_CASES = [
+    # (kv, qpk, head_dim, rotary, style, dtype, tokens)
+    (2, 4, 128, 128, "half", torch.bfloat16, 4096),
+    (8, 5, 128, 128, "half", torch.bfloat16, 1000),
+    (2, 8, 256, 64, "half", torch.bfloat16, 700),
+    (8, 5, 128, 128, "half", torch.float16, 333),
+    (2, 4, 64, 64, "interleaved", torch.bfloat16, 257),
+    (1, 8, 256, 64, "half", torch.bfloat16, 130),
+    (4, 1, 128, 128, "half", torch.bfloat16, 129),
+    (16, 2, 64, 64, "half", torch.bfloat16, 300),
+]
+
+
+@pytest.mark.parametrize("case", SCORE_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5])[-4:]}t{c[6]}" for c in SCORE_CASES])
+def test_score_paged_matches_oracle(hip_device, case) -> None:
+    kernels, _, _ = _kvc()
+    kv, qpk, head_dim, rotary, style, dtype, tokens = case
+    g = torch.Generator().manual_seed(sum(case[:4]) + tokens)
+    freq = rotary // 2
+    stats = _random_stats(g, kv, qpk, freq, head_dim - rotary, rotary, style=style)
+    n_blocks = -(-tokens // 128)
+    pool = n_blocks + 5
+    cache = torch.randn(pool, 128, kv, head_dim, generator=g).to(dtype)
+    blocks = torch.randperm(pool, generator=g)[:n_blocks]
+    offsets = ref.build_geometric_offsets(32768)
+    round_start = tokens + 17
+    keys = ref.gather_paged_range(cache, blocks, start=0, count=tokens, block_size=128)
+    want = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets)
+
+    # Direct phase table (torch-path semantics) through the batched entry point.
+    cos, sin = kernels.mean_phase_table(
+        torch.tensor([round_start], dtype=torch.int64, device=hip_device), offsets.to(hip_device), stats.omega.view(1, -1).to(hip_device)
+    )
+    out = torch.full((kv, qpk, tokens + 3), float("nan"), device=hip_device)
+    d = lambda t: None if t is None else t.to(hip_device)  # noqa: E731
+    assert kernels.score_paged_keys_mean_precomputed(
+        cache.to(hip_device),
+        blocks.to(hip_device),
+        d(stats.q_mean_real),
+        d(stats.q_mean_imag),
+        d(torch.sqrt(stats.freq_scale_sq)),
+        d(stats.q_abs_mean - torch.sqrt(stats.q_mean_real.square() + stats.q_mean_imag.square() + 1e-8)),
+        cos.view(-1),
+        sin.view(-1),
+        tokens,
+        out,
+        128,
+        style,
+        q_pass_mean=d(stats.q_pass_mean),
+        rotary_dim=rotary if rotary != head_dim else None,
+    )
+    got = out.cpu()
+    assert torch.isnan(got[..., tokens:]).all(), "scorer wrote past num_tokens"
+    assert_scores_close(got[..., :tokens].reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
+
+
+def test_reference_smoke_inputs_with_shifted_phases(hip_device) -> None:
+    # The reference device smoke (tests/run_npu_kernel_smoke.py:83-138) widened to
+    # a 16-dim head: linspace keys and statistics, angle-addition phases at
+    # round_start 300, compared with the torch path at rtol = atol = 2e-3.
+    kernels, _, _ = _kvc()
+    kv, qpk, freq = 2, 2, 8
+    cache = torch.linspace(-1.0, 1.0, 3 * 128 * kv * 2 * freq).view(3, 128, kv, 2 * freq).to(torch.bfloat16)
+    blocks = torch.tensor([2, 0])
+    qr = torch.linspace(0.1, 0.8, kv * qpk * freq).view(kv, qpk, freq)
+    qi = torch.linspace(-0.4, 0.3, kv * qpk * freq).view(kv, qpk, freq)
+    qa = torch.sqrt(qr.square() + qi.square()) + 0.2
+    fscale = torch.linspace(0.8, 1.2, kv * qpk * freq).view(kv, qpk, freq)
+    omega = torch.logspace(0, -3, freq)
+    offsets = torch.tensor([1.0, 2.0, 4.0])
+    extra = qa - torch.sqrt(qr.square() + qi.square() + 1e-8)
+    out = torch.empty(kv, qpk, 256, device=hip_device)
+    d = lambda t: t.to(hip_device)  # noqa: E731
+    assert kernels.score_paged_keys_mean(
+        d(cache), d(blocks), d(qr), d(qi), d(fscale), d(extra), d(omega),
+        d(torch.cos(offsets.unsqueeze(1) * omega).mean(0)), d(torch.sin(offsets.unsqueeze(1) * omega).mean(0)),
+        300, 256, out, 128, "half",
+    )
+    keys = ref.gather_paged_range(cache, blocks, start=0, count=256, block_size=128)
+    want = ref.score_post_rope_keys(keys, ref.LayerStats(qr, qi, qa, fscale.square(), omega), round_start=300, offsets=offsets)
+    torch.testing.assert_close(out.cpu(), want, rtol=2e-3, atol=2e-3)
+
+
+def test_aggregate_single_layer_rsqrt_form(hip_device) -> None:
+    kernels, _, _ = _kvc()
+    g = torch.Generator().manual_seed(9)
+    scores = torch.randn(2, 2, 256, generator=g) * 3 + 1
+    var, mean = torch.var_mean(scores, dim=-1, correction=0)
+    agg = torch.empty(256, device=hip_device)
+    assert kernels.aggregate_normalized_scores(
+        scores.to(hip_device), mean.to(hip_device), var.to(hip_device), agg, 256, layer_aggregation="mean", first_layer=True
+    )
+    want = ((scores - mean.unsqueeze(-1)) * torch.rsqrt(var.unsqueeze(-1) + 1e-6)).amax(dim=(0, 1))
+    torch.testing.assert_close(agg.cpu(), want, rtol=2e-3, atol=2e-3)
+    second = torch.randn(2, 2, 256, generator=g)
+    v2, m2 = torch.var_mean(second, dim=-1, correction=0)
+    assert kernels.aggregate_normalized_scores(
+        second.to(hip_device), m2.to(hip_device), v2.to(hip_device), agg, 256, layer_aggregation="max", first_layer=False
+    )
+    want2 = torch.maximum(want, ((second - m2.unsqueeze(-1)) * torch.rsqrt(torch.clamp(v2, min=1e-6).unsqueeze(-1))).amax(dim=(0, 1)))
+    torch.testing.assert_close(agg.cpu(), want2, rtol=2e-3, atol=2e-3)
+
+
+# ----------------------------------------------------------------- select --
+
+
+def test_select_reference_kats(hip_device) -> None:
+    _, selection, _ = _kvc()
+    keep = selection.select_keep_indices(
+        torch.tensor([10.0, 9.0, 8.0, 7.0, -5.0, -6.0], device=hip_device),
+        budget=4, protected_prefix=0, protected_recent=2, segments=8, policy="global",
+    )
+    assert keep.cpu().tolist() == [0, 1, 4, 5]
+    keep = selection.select_keep_indices(
+        torch.arange(16, dtype=torch.float32, device=hip_device), budget=12, protected_prefix=2, protected_recent=2, segments=4, policy="v3"
+    )
+    assert set(range(16)) - set(keep.cpu().tolist()) == {2, 5, 8, 11}
+    keep = selection.select_keep_indices(torch.zeros(19, device=hip_device), budget=13, protected_prefix=2, protected_recent=2, segments=8, policy="v3")
+    assert keep.numel() == 13 and {0, 1, 17, 18} <= set(keep.cpu().tolist())
+
+
+SELECT_CASES = [
+    # (n, budget, prefix, recent, segments, policy, ties)
+    (4096, 2048, 0, 128, 8, "global", False),
+    (16384, 4096, 0, 128, 8, "global", False),
+    (36001, 4608, 128, 512, 8, "v3", False),
+    (5000, 4608, 128, 512, 8, "v3", True),
+    (3000, 1000, 7, 33, 3, "global", True),
+    (131072, 4608, 0, 256, 8, "global", False),
+    (1000, 1000, 0, 128, 8, "global", False),
+    (300, 128, 0, 0, 8, "v3", True),
+    (19, 13, 2, 2, 8, "v3", False),
+]
+
+
+@pytest.mark.parametrize("case", SELECT_CASES)
+def test_select_matches_stable_brute_force(hip_device, case) -> None:
+    _, selection, _ = _kvc()
+    n, budget, prefix, recent, segments, policy, ties = case
+    g = torch.Generator().manual_seed(n + budget)
+    scores = torch.randn(n, generator=g)
+    if ties:
+        scores = torch.round(scores * 4) / 4  # heavy ties
+    keep = selection.select_keep_indices(
+        scores.to(hip_device), budget=budget, protected_prefix=prefix, protected_recent=recent, segments=segments, policy=policy
+    ).cpu()
+    want = brute.select_stable(scores.numpy(), budget, prefix, recent, segments, policy)
+    np.testing.assert_array_equal(keep.numpy(), want)
+    if not ties:
+        oracle = ref.select_keep_indices(
+            scores, budget=budget, protected_prefix=prefix, protected_recent=recent, segments=segments, policy=policy
+        )
+        assert torch.equal(keep, oracle)
+
+
+def test_select_special_values(hip_device) -> None:
+    _, selection, _ = _kvc()
+    scores = torch.tensor([0.0, -0.0, float("nan"), float("inf"), 1.0, 1.0, float("-inf"), -3.0])
+    for budget in range(1, 9):
+        keep = selection.select_keep_indices(
+            scores.to(hip_device), budget=budget, protected_prefix=0, protected_recent=0, segments=1, policy="global"
+        ).cpu()
+        np.testing.assert_array_equal(keep.numpy(), brute.select_stable(scores.numpy(), budget, 0, 0, 1, "global"))
+
+
+def test_select_rejects_invalid_arguments(hip_device) -> None:
+    _, selection, _ = _kvc()
+    s = torch.zeros(10, device=hip_device)
+    with pytest.raises(ValueError):
+        selection.select_keep_indices(s, budget=11, protected_prefix=0, protected_recent=0, segments=1, policy="global")
+    with pytest.raises(ValueError):
+        selection.select_keep_indices(s, budget=4, protected_prefix=3, protected_recent=2, segments=1, policy="global")
+    with pytest.raises(ValueError):
+        selection.select_keep_indices(s.cpu(), budget=4, protected_prefix=0, protected_recent=0, segments=1, policy="global")
+
+
+# ---------------------------------------------------------------- compact --
+
+
+def _layers(g, n_layers, pages, kv, dim, dtype):
+    ks = [torch.randn(pages, 128, kv, dim, generator=g).to(dtype) for _ in range(n_layers)]
+    vs = [torch.randn(pages, 128, kv, dim, generator=g).to(dtype) for _ in range(n_layers)]
+    return ks, vs
+
+
+@pytest.mark.parametrize("mode", ["private", "inplace"])
+@pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided"])
+def test_compact_bit_exact(hip_device, mode: str, pattern: str) -> None:
+    _, _, cache = _kvc()
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    g = torch.Generator().manual_seed(len(mode) * 7 + len(pattern))
+    kv, dim, n_layers, budget = 4, 128, 3, 640
+    lens = [2000, 1500, 641]
+    src_tables, dst_tables = [], []
+    pool = sum(-(-n // 128) for n in lens) + (0 if mode == "inplace" else 5 * len(lens)) + 3
+    perm = torch.randperm(pool, generator=g).tolist()
+    cur = 0
+    for n in lens:
+        nb = -(-n // 128)
+        src_tables.append(perm[cur : cur + nb])
+        cur += nb
+    if mode == "private":
+        for _ in lens:
+            dst_tables.append(perm[cur : cur + 5])
+            cur += 5
+    keeps = []
+    for n in lens:
+        if pattern == "random":
+            k = torch.sort(torch.randperm(n, generator=g)[:budget]).values
+        elif pattern == "front":
+            k = torch.arange(budget)
+        elif pattern == "tail":
+            k = torch.arange(n - budget, n)
+        else:
+            k = torch.linspace(0, n - 1, budget).round().long().unique()
+            while k.numel() < budget:
+                k = torch.unique(torch.cat([k, torch.randint(0, n, (budget,), generator=g)]))[:budget]
+            k = torch.sort(k[:budget]).values
+        keeps.append(k)
+    ks, vs = _layers(g, n_layers, pool, kv, dim, torch.bfloat16)
+    ks_d = [k.to(hip_device) for k in ks]
+    vs_d = [v.to(hip_device) for v in vs]
+    # Oracle: reference materialisation per sequence and layer.
+    for b, n in enumerate(lens):
+        dst = torch.tensor(dst_tables[b] if mode == "private" else src_tables[b][: -(-budget // 128)])
+        ref.method_compress(ks, vs, torch.tensor(src_tables[b]), dst, keeps[b], budget)
+    so, si, slen = dev.ragged(src_tables, hip_device)
+    do = di = None
+    if mode == "private":
+        do, di, _ = dev.ragged(dst_tables, hip_device)
+    keep = torch.stack(keeps).to(hip_device)
+    cache.compact_layers(
+        dev.pointer_table(ks_d, hip_device),
+        dev.pointer_table(vs_d, hip_device),
+        num_pages=pool,
+        page_stride=int(ks_d[0].stride(0)),
+        row_elems=kv * dim,
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=hip_device),
+        src_block_offsets=so,
+        src_block_ids=si,
+        dst_block_offsets=do,
+        dst_block_ids=di,
+        keep=keep,
+        budget=budget,
+    )
+    torch.cuda.synchronize()
+    for layer in range(n_layers):
+        assert torch.equal(ks_d[layer].cpu(), ks[layer]), f"K layer {layer} differs"
+        assert torch.equal(vs_d[layer].cpu(), vs[layer]), f"V layer {layer} differs"
+    tables, freed = cache.rewrite_block_tables(
+        budget=budget, src_block_offsets=so, src_block_ids=si, src_lengths=slen, dst_block_offsets=do, dst_block_ids=di
+    )
+    for b in range(len(lens)):
+        want_table, want_freed = ref.rewrite_block_table(src_tables[b], dst_tables[b] if mode == "private" else None, budget)
+        assert tables[b].cpu().tolist() == want_table
+        assert freed[b].cpu().tolist() == want_freed
+
+
+def test_materialize_token_slots_padded_pages(hip_device) -> None:
+    # tests/test_cache.py:50-94 with 128-token blocks: K and V interleaved in one
+    # padded buffer; the padding must stay untouched.
+    _, _, cache = _kvc()
+    bs, pages, heads, dim = 128, 4, 1, 8
+    logical = bs * heads * dim
+    stride = 2 * logical + 4
+    raw = torch.full((pages * stride,), -1, dtype=torch.float16, device=hip_device)
+    shape, strides = (pages, bs, heads, dim), (stride, heads * dim, dim, 1)
+    k = torch.as_strided(raw, shape, strides)
+    v = torch.as_strided(raw, shape, strides, storage_offset=logical)
+    k.copy_(torch.arange(pages * logical, device=hip_device).view(shape))
+    v.copy_((torch.arange(pages * logical, device=hip_device) % 1000 + 100).view(shape))
+    src = torch.tensor([2, 0, 3], device=hip_device)
+    keep = torch.sort(torch.randperm(384, generator=torch.Generator().manual_seed(3))[:128]).values.to(hip_device)
+    kh, vh = k.cpu(), v.cpu()
+    want_k = ref.gather_paged_tokens(kh, src.cpu(), keep.cpu(), bs)
+    want_v = ref.gather_paged_tokens(vh, src.cpu(), keep.cpu(), bs)
+    cache.materialize_selected_tokens(k, v, src, torch.tensor([2], device=hip_device), keep, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(k[2].cpu(), want_k) and torch.equal(v[2].cpu(), want_v)
+    assert torch.equal(raw.view(pages, stride)[:, -4:].cpu(), torch.full((pages, 4), -1, dtype=torch.float16))
+
+
+def test_token_slots_and_expand(hip_device) -> None:
+    _, _, cache = _kvc()
+    blocks = torch.tensor([2, 0], device=hip_device)
+    got = cache.token_slots(blocks, torch.tensor([0, 3, 4, 7, 130, 255], device=hip_device), 128)
+    assert got.cpu().tolist() == [256, 259, 260, 263, 2, 127]
+    ids = torch.tensor([3, 1], device=hip_device)
+    assert cache.expand_scheduler_block_ids(ids, 16).cpu().tolist() == [48 + j for j in range(16)] + [16 + j for j in range(16)]
+    assert cache.expand_scheduler_block_ids(ids, 1).cpu().tolist() == [3, 1]

@@ -1,0 +1,201 @@
+"""End-to-end parity of the batched compression step and the method API (GPU)."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_agg_close, assert_keep_matches, assert_scores_close, oracle_stats
+from oracle import triattention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _oracle_for(host, spec, b):
+    stats = host.calibration.to_device(spec.model_shape(), torch.device("cpu"))
+    layer_stats = [oracle_stats(stats[layer]) for layer in spec.scoring_layers]
+    cfg = ref.MethodConfig(
+        budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
+        score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
+    )
+    return ref.method_select(
+        [host.k_caches[layer] for layer in spec.scoring_layers],
+        layer_stats,
+        host.source_tables[b],
+        spec.seq_lens[b],
+        host.round_starts[b],
+        ref.build_geometric_offsets(spec.max_model_len),
+        cfg,
+    )
+
+
+def _protected(n, spec):
+    mask = torch.zeros(n, dtype=torch.bool)
+    p = min(spec.prefix, n)
+    r = min(spec.recent, n - p)
+    mask[:p] = True
+    if r:
+        mask[n - r :] = True
+    return mask
+
+
+def _run_and_check(spec, hip_device, *, check_layers=None):
+    from kvcompress_mi355x import workloads
+
+    host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
+    cache = workloads.move_cache(host, hip_device)
+    pipeline, batch = workloads.build_pipeline(cache)
+    keep, tables, freed = pipeline.step(batch)
+    torch.cuda.synchronize()
+    offs = [0]
+    for n in spec.seq_lens:
+        offs.append(offs[-1] + n)
+    h_q = spec.num_attention_heads
+    near_ties = 0
+    oracle_keeps = []
+    for b, n in enumerate(spec.seq_lens):
+        out = _oracle_for(host, spec, b)
+        for s_idx in range(len(spec.scoring_layers)):
+            got_raw = pipeline.raw[s_idx, offs[b] : offs[b + 1], :h_q].t()
+            assert_scores_close(got_raw, out["raw"][s_idx].reshape(h_q, n))
+            var, mean = out["stats"][s_idx]
+            torch.testing.assert_close(pipeline.mean[s_idx, b].cpu(), mean.reshape(-1), rtol=1e-4, atol=1e-4)
+            torch.testing.assert_close(pipeline.var[s_idx, b].cpu(), var.reshape(-1), rtol=1e-3, atol=1e-4)
+        assert_agg_close(pipeline.agg[offs[b] : offs[b + 1]], out["agg"])
+        near_ties += assert_keep_matches(keep[b], out["keep"], out["agg"], spec.budget, _protected(n, spec))
+        oracle_keeps.append(out["keep"])
+    # Compaction is bit-exact given the kernel's own keep set.
+    layers = range(spec.n_layers) if check_layers is None else check_layers
+    nb = -(-spec.budget // 128)
+    for b in range(len(spec.seq_lens)):
+        gkeep = keep[b].cpu()
+        src = host.source_tables[b]
+        dst = src[:nb] if spec.inplace else host.destination_tables[b]
+        slots = ref.token_slots(src, gkeep, 128)
+        for layer in layers:
+            want_k = ref.gather_slots(host.k_caches[layer], slots)
+            want_v = ref.gather_slots(host.v_caches[layer], slots)
+            dslots = ref.token_slots(dst.to(hip_device), torch.arange(spec.budget, device=hip_device), 128)
+            got_k = cache.k_caches[layer].view(-1, spec.num_kv_heads, spec.head_dim)[dslots].cpu()
+            got_v = cache.v_caches[layer].view(-1, spec.num_kv_heads, spec.head_dim)[dslots].cpu()
+            assert torch.equal(got_k, want_k), f"K layer {layer} seq {b}"
+            assert torch.equal(got_v, want_v), f"V layer {layer} seq {b}"
+        want_table, want_freed = ref.rewrite_block_table(src.tolist(), None if spec.inplace else dst.tolist(), spec.budget)
+        assert tables[b].cpu().tolist() == want_table
+        assert freed[b].cpu().tolist() == want_freed
+    return pipeline, keep, oracle_keeps, near_ties
+
+
+def test_config1_end_to_end(hip_device) -> None:
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(1)
+    pipeline, keep, oracle_keeps, near = _run_and_check(spec, hip_device)
+    assert near <= 2
+    fixture = json.loads((GOLDEN / "config1_expected.json").read_text())
+    assert fixture["keep_sha256"] is not None
+    assert sorted(keep[0].cpu().tolist()) == keep[0].cpu().tolist()
+    golden_keep = np.load(GOLDEN / "config1_keep.npy", allow_pickle=False)
+    diff = set(keep[0].cpu().tolist()) ^ set(golden_keep.tolist())
+    assert len(diff) <= 2 * near
+
+
+def test_ragged_batch_private(hip_device) -> None:
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(
+        2, n_layers=4, score_layer_stride=2, seq_lens=(4224, 5000, 8192, 4351), budget=4096, recent=128, max_model_len=32768
+    )
+    _run_and_check(spec, hip_device)
+
+
+def test_partial_rope_v3_hybrid_pages(hip_device) -> None:
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(3, n_layers=4, seq_lens=(9000, 6000))
+    _run_and_check(spec, hip_device)
+
+
+def test_inplace_front_pages_with_outliers(hip_device) -> None:
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(4, n_layers=2, score_layer_stride=1, seq_lens=(12000, 20000), pool_pages=300, max_model_len=32768)
+    _run_and_check(spec, hip_device)
+
+
+def test_fp16_decode_shape(hip_device) -> None:
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(5, n_layers=2, score_layer_stride=1, seq_lens=(4300, 7000, 4224))
+    _run_and_check(spec, hip_device)
+
+
+def test_method_api_compress(hip_device, tmp_path) -> None:
+    """TriAttentionMethod through method API v1 on a bound synthetic cache."""
+    from kvcompress_mi355x.methods import create_method
+    from kvcompress_mi355x.methods.base import CompressionRequest, LayerCache
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(2, n_layers=4, score_layer_stride=2, seq_lens=(6000,), budget=2048, recent=128, max_model_len=16384)
+    host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
+    cache = workloads.move_cache(host, hip_device)
+    stats_path = tmp_path / "stats.pt"
+    torch.save(
+        {
+            "metadata": dict(host.calibration.metadata),
+            "layer_stats": {
+                i: {
+                    "q_mean_real": s.q_mean_real,
+                    "q_mean_imag": s.q_mean_imag,
+                    "q_abs_mean": s.q_abs_mean,
+                    "freq_scale_sq": s.freq_scale_sq,
+                }
+                for i, s in host.calibration.layers.items()
+            },
+        },
+        stats_path,
+    )
+    vllm_config = SimpleNamespace(
+        parallel_config=SimpleNamespace(tensor_parallel_size=1),
+        model_config=SimpleNamespace(max_model_len=spec.max_model_len),
+        speculative_config=None,
+    )
+    method = create_method(
+        "triattention",
+        {"stats_path": str(stats_path), "kv_budget": 2048, "score_layer_stride": 2, "protected_recent_window": 128},
+        vllm_config,
+        spec.model_shape(),
+    )
+    assert method.compatibility_reasons(None) == ()
+    assert method.runtime_spec.compression_threshold_tokens == 2176
+    layers = tuple(LayerCache(f"model.layers.{i}.self_attn.attn", i, cache.k_caches[i], cache.v_caches[i]) for i in range(spec.n_layers))
+    method.bind_model_runner(SimpleNamespace(device=hip_device), layers)
+    src = cache.source_tables[0]
+    dst = cache.destination_tables[0]
+    request = CompressionRequest(
+        request_id="r0",
+        semantic_num_tokens=6000,
+        physical_num_tokens=6000,
+        source_block_ids=(tuple(src.cpu().tolist()),),
+        destination_block_ids=(tuple(dst.cpu().tolist()),),
+        source_block_ids_device=src,
+        destination_block_ids_device=dst,
+    )
+    keep_only = method.select_keep_indices(src, 6000, 6000)
+    result = method.compress(request)
+    torch.cuda.synchronize()
+    assert result.physical_num_tokens == 2048
+    assert result.per_layer_physical_num_tokens == tuple((layer.name, 2048) for layer in layers)
+    out = _oracle_for(host, spec, 0)
+    assert_keep_matches(keep_only, out["keep"], out["agg"], 2048, _protected(6000, spec))
+    slots = ref.token_slots(src.cpu(), keep_only.cpu(), 128)
+    dslots = ref.token_slots(dst, torch.arange(2048, device=hip_device), 128)
+    for i in range(spec.n_layers):
+        assert torch.equal(cache.k_caches[i].view(-1, 8, 128)[dslots].cpu(), ref.gather_slots(host.k_caches[i], slots))

@@ -1,0 +1,290 @@
+"""Host-side contracts of the method boundary (no GPU): options, registry,
+calibration loading, cache validation and the C-ABI library's exports."""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from kvcompress_mi355x.methods.base import (
+    CompressionRequest,
+    CompressionResult,
+    KVCompressionMethod,
+    LayerCache,
+    MethodRuntimeSpec,
+    ModelShape,
+)
+from kvcompress_mi355x.methods.registry import MethodRegistry
+from kvcompress_mi355x.methods.triattention import TriAttentionConfig
+from kvcompress_mi355x.methods.triattention import method as tri_method
+from kvcompress_mi355x.methods.triattention.stats import CalibrationStats, LayerCalibrationStats
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+# ----------------------------------------------------------------- config --
+
+
+def test_config_accepts_documented_values() -> None:
+    config = TriAttentionConfig.from_method_config(
+        {
+            "stats_path": "/tmp/stats.pt",
+            "kv_budget": 2048,
+            "recompute_window": 128,
+            "position_policy": "v3",
+            "protected_prefix_window": 128,
+            "protected_recent_window": 64,
+            "position_segments": 8,
+            "score_aggregation": "max",
+            "layer_aggregation": "mean",
+            "score_chunk_size": 512,
+            "score_layer_stride": 8,
+            "min_output_tokens_for_compression": 64,
+            "auto_calibrate": True,
+            "calibration_input_path": "/tmp/calibration.txt",
+            "calibration_max_length": 8192,
+            "calibration_device": "cuda:0",
+            "calibration_attn_implementation": "eager",
+            "calibration_local_files_only": True,
+        }
+    )
+    assert config.stats_path == Path("/tmp/stats.pt")
+    assert config.compression_threshold_tokens == 2176
+    assert config.position_policy == "v3" and config.protected_prefix_window == 128
+    assert config.calibration_input_path == Path("/tmp/calibration.txt")
+
+
+@pytest.mark.parametrize(
+    ("option", "value"),
+    [
+        ("kv_budget", 2000),
+        ("recompute_window", 0),
+        ("score_chunk_size", 129),
+        ("score_layer_stride", 0),
+        ("min_output_tokens_for_compression", -1),
+        ("protected_prefix_window", -1),
+        ("protected_recent_window", -1),
+        ("position_segments", 0),
+        ("position_policy", "unknown"),
+        ("score_aggregation", "median"),
+        ("auto_calibrate", 1),
+        ("calibration_max_length", 127),
+        ("calibration_attn_implementation", "unknown"),
+        ("kv_budget", True),
+    ],
+)
+def test_config_rejects_invalid_values(option: str, value: object) -> None:
+    with pytest.raises(ValueError):
+        TriAttentionConfig.from_method_config({"stats_path": "/tmp/stats.pt", option: value})
+
+
+def test_config_rejects_unknown_option_and_windows_over_budget() -> None:
+    with pytest.raises(ValueError, match="unknown"):
+        TriAttentionConfig.from_method_config({"stats_path": "/tmp/stats.pt", "typo": 1})
+    with pytest.raises(ValueError):
+        TriAttentionConfig.from_method_config(
+            {"stats_path": "/tmp/s.pt", "kv_budget": 256, "protected_prefix_window": 200, "protected_recent_window": 100}
+        )
+
+
+# --------------------------------------------------------------- registry --
+
+
+class _Method(KVCompressionMethod):
+    @property
+    def name(self) -> str:
+        return "test_method"
+
+    @property
+    def runtime_spec(self) -> MethodRuntimeSpec:
+        return MethodRuntimeSpec(True, 256, 128, 128)
+
+    def compatibility_reasons(self, worker: object) -> tuple[str, ...]:
+        return ()
+
+    def bind_model_runner(self, runner: object, layer_caches: tuple[LayerCache, ...]) -> None:
+        return None
+
+    def compress(self, request: CompressionRequest) -> CompressionResult:
+        return CompressionResult(physical_num_tokens=128)
+
+
+def _shape() -> ModelShape:
+    return ModelShape("qwen2", 1, 1, 1, 128, 10_000.0, False)
+
+
+def test_registry_creates_and_rejects() -> None:
+    registry = MethodRegistry()
+    registry.register("test_method", lambda o, c, s: _Method())
+    method = registry.create("test_method", {}, SimpleNamespace(), _shape())
+    assert isinstance(method, _Method) and method.query_window_tokens == 0
+    assert registry.names() == ("test_method",)
+    with pytest.raises(ValueError, match="already registered"):
+        registry.register("test_method", lambda o, c, s: _Method())
+    with pytest.raises(ValueError, match="available: test_method"):
+        registry.create("missing", {}, SimpleNamespace(), _shape())
+    registry.register("broken", lambda o, c, s: object())  # type: ignore[arg-type,return-value]
+    with pytest.raises(TypeError, match="expected KVCompressionMethod"):
+        registry.create("broken", {}, SimpleNamespace(), _shape())
+    registry.register("renamed", lambda o, c, s: _Method())
+    with pytest.raises(ValueError, match="returned method named"):
+        registry.create("renamed", {}, SimpleNamespace(), _shape())
+
+
+def test_builtin_method_registered_and_api_version() -> None:
+    import kvcompress_mi355x
+
+    assert "triattention" in kvcompress_mi355x.available_methods()
+    assert kvcompress_mi355x.METHOD_API_VERSION == 1
+
+
+def test_mtp_layer_names_and_gqa_width() -> None:
+    assert tri_method.is_mtp_cache_layer("mtp.layers.0.self_attn.attn")
+    assert tri_method.is_mtp_cache_layer("draft_model.mtp.layers.1.self_attn.attn")
+    assert not tri_method.is_mtp_cache_layer("language_model.model.layers.3.self_attn.attn")
+    shape = ModelShape("qwen3_5_moe_text", 40, 16, 2, 256, 1e7, False, 64, tuple(range(3, 40, 4)))
+    assert tri_method.queries_per_kv_head(shape) == 8
+
+
+# ------------------------------------------------------------ calibration --
+
+
+def _write_flat(path: Path, layers: int = 2, heads: int = 4) -> None:
+    stats = {
+        f"layer{l:02d}_head{h:02d}": {
+            "q_mean_real": torch.full((4,), float(l + h)),
+            "q_mean_imag": torch.zeros(4),
+            "q_abs_mean": torch.ones(4),
+        }
+        for l in range(layers)
+        for h in range(heads)
+    }
+    torch.save({"metadata": {"head_dim": 8, "rope_style": "half", "rope_type": "default"}, "stats": stats}, path)
+
+
+def test_flat_stats_load_and_group(tmp_path: Path) -> None:
+    _write_flat(tmp_path / "s.pt")
+    cal = CalibrationStats.load(tmp_path / "s.pt")
+    model = ModelShape("qwen3", 2, 4, 2, 8, 10000.0, False)
+    assert cal.validate(model) == ()
+    dev = cal.to_device(model, torch.device("cpu"))
+    assert dev[0].q_mean_real.shape == (2, 2, 4) and dev[1].omega.shape == (4,)
+    torch.testing.assert_close(dev[1].q_mean_real[1, 0], torch.full((4,), 3.0))
+
+
+def test_incomplete_heads_fail_closed(tmp_path: Path) -> None:
+    _write_flat(tmp_path / "s.pt", layers=1, heads=2)
+    payload = torch.load(tmp_path / "s.pt", weights_only=True)
+    del payload["stats"]["layer00_head00"]
+    torch.save(payload, tmp_path / "s.pt")
+    with pytest.raises(ValueError, match="complete and contiguous"):
+        CalibrationStats.load(tmp_path / "s.pt")
+
+
+def test_scaled_rope_needs_exact_stats(tmp_path: Path) -> None:
+    _write_flat(tmp_path / "s.pt", layers=1, heads=2)
+    reasons = CalibrationStats.load(tmp_path / "s.pt").validate(ModelShape("qwen3", 1, 2, 1, 8, 10000.0, True))
+    assert any("inv_freq" in r for r in reasons) and any("freq_scale_sq" in r for r in reasons)
+
+
+def test_invalid_values_fail_closed() -> None:
+    cal = CalibrationStats(
+        metadata={"head_dim": 8, "rope_style": "half"},
+        layers={
+            0: LayerCalibrationStats(
+                q_mean_real=torch.tensor([[float("nan"), 0.0, 0.0, 0.0]]),
+                q_mean_imag=torch.zeros(1, 4),
+                q_abs_mean=torch.tensor([[-1.0, 1.0, 1.0, 1.0]]),
+                freq_scale_sq=torch.tensor([[0.0, 1.0, 1.0, 1.0]]),
+            )
+        },
+    )
+    reasons = cal.validate(ModelShape("qwen3", 1, 1, 1, 8, 10000.0, False))
+    assert any("non-finite" in r for r in reasons)
+    assert any("negative" in r for r in reasons)
+    assert any("freq_scale_sq must be positive" in r for r in reasons)
+
+
+def test_partial_rope_stats_and_tp_shard() -> None:
+    layer = LayerCalibrationStats(
+        q_mean_real=torch.arange(16 * 32, dtype=torch.float32).reshape(16, 32),
+        q_mean_imag=torch.zeros(16, 32),
+        q_abs_mean=torch.ones(16, 32),
+        freq_scale_sq=torch.ones(1, 32),
+        inv_freq=torch.ones(32),
+        q_pass_mean=torch.ones(16, 192),
+    )
+    cal = CalibrationStats(
+        metadata={"model_type": "qwen3_5_moe_text", "num_layers": 8, "head_dim": 256, "rotary_dim": 64,
+                  "attention_layer_indices": [3, 7], "rope_style": "half"},
+        layers={3: layer, 7: layer},
+    )
+    model = ModelShape("qwen3_5_moe_text", 8, 16, 2, 256, 1e7, False, 64, (3, 7))
+    assert cal.validate(model) == ()
+    dev = cal.to_device(model, torch.device("cpu"))
+    assert set(dev) == {3, 7} and dev[3].q_mean_real.shape == (2, 8, 32) and dev[3].q_pass_mean.shape == (2, 8, 192)
+    r0 = cal.to_device(model, torch.device("cpu"), tensor_parallel_rank=0, tensor_parallel_size=2)[3]
+    r1 = cal.to_device(model, torch.device("cpu"), tensor_parallel_rank=1, tensor_parallel_size=2)[3]
+    assert r0.q_mean_real.shape == (1, 8, 32) and not torch.equal(r0.q_mean_real, r1.q_mean_real)
+
+
+def test_kv_head_stats_expand_across_group() -> None:
+    cal = CalibrationStats(
+        metadata={"head_dim": 8, "rope_style": "half"},
+        layers={0: LayerCalibrationStats(torch.tensor([[1.0, 2, 3, 4], [5, 6, 7, 8]]), torch.zeros(2, 4), torch.ones(2, 4), torch.full((2, 4), 4.0))},
+    )
+    model = ModelShape("qwen3", 1, 4, 2, 8, 10000.0, False)
+    assert cal.validate(model) == ()
+    g = cal.to_device(model, torch.device("cpu"))[0]
+    torch.testing.assert_close(g.q_mean_real[0, 0], g.q_mean_real[0, 1])
+    torch.testing.assert_close(g.freq_scale_sq, torch.full((2, 2, 4), 4.0))
+
+
+# --------------------------------------------------------- device checks --
+
+
+def test_product_path_rejects_host_tensors() -> None:
+    from kvcompress_mi355x.methods.triattention import selection
+
+    with pytest.raises(ValueError, match="HIP device"):
+        selection.select_keep_indices(torch.zeros(10), budget=4, protected_prefix=0, protected_recent=0, segments=1, policy="global")
+
+
+def test_cache_validation_matches_reference_contract() -> None:
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    with pytest.raises(ValueError):
+        dev.validate_cache(torch.zeros(2, 128, 1, 8), "k")  # host tensor
+
+
+# ------------------------------------------------------------------ C ABI --
+
+
+def test_library_exports_every_header_symbol() -> None:
+    from kvcompress_mi355x import _native
+
+    header = (REPO / "include" / "kvcompress_mi355x.h").read_text()
+    declared = set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(kvc_\w+)\s*\(", header, flags=re.M))
+    assert declared, "no declarations parsed from the header"
+    assert declared == set(_native.SIGNATURES), "binding table and header disagree"
+    lib = _native.load()
+    for name in declared:
+        assert hasattr(lib, name), f"{name} not exported"
+    assert lib.kvc_abi_version() == _native.ABI_VERSION
+
+
+def test_workspace_query_and_argument_validation_without_gpu() -> None:
+    from kvcompress_mi355x import _native
+
+    lib = _native.load()
+    assert lib.kvc_score_workspace_bytes(6, 8, 128, 128, 5, 16, 16384) > 0
+    assert lib.kvc_score_workspace_bytes(1, 2, 8, 8, 2, 1, 10) == 0  # rotary 8 is not a multiple of 16
+    assert lib.kvc_score_workspace_bytes(1, 2, 128, 128, 9, 1, 10) == 0  # qpk > 8
+    with pytest.raises(ValueError, match="budget"):
+        _native.call("kvc_select_keep", None, 1, 10, None, None, None, 20, 0, 0, 1, 0, None, 20)
+    with pytest.raises(ValueError):
+        _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4)

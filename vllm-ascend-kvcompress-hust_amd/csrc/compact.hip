@@ -1,0 +1,337 @@
+// KV compaction on CDNA4: kept K/V rows -> destination rows, all layers in one launch.
+//
+// Row i (< budget) of sequence b's destination receives source row keep[b][i].
+// A row is the kv_heads*head_dim elements of one token, contiguous inside its
+// page (reference cache layout [pages][128][kv_heads][head_dim]).  A
+// workgroup moves a tile of rows x a slice of columns in `Chunk`-sized words;
+// each thread issues all of its loads for the tile before its stores so a
+// lane keeps several requests in flight.
+//
+// Private mode (destination pages disjoint from the source pages): every tile
+// is independent; the grid spans (row tile x column slice, sequence,
+// layer x {K,V}).
+//
+// In-place mode (destinations are the sequence's own front pages): keep is
+// strictly increasing, so keep[j] >= j and the source row of destination j can
+// only be overwritten by a destination i >= j.  A workgroup therefore owns one
+// column slice of one (layer, K/V, sequence) and walks the rows in ascending
+// tiles: all loads of a tile complete before a workgroup barrier, then the
+// tile's stores go out.  A row read by tile T lies at index >= the first row
+// of tile T, so it is overwritten, if at all, by tile T itself (after the
+// barrier) or a later tile.  Column slices are disjoint bytes, so slices run
+// in parallel.  Rows whose source and destination coincide are skipped.
+
+#include "kvc_common.h"
+
+namespace kvc {
+namespace {
+
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 8;  // rows in flight per thread
+
+struct CompactArgs {
+  const uint64_t* k_ptrs;
+  const uint64_t* v_ptrs;
+  int64_t num_pages;
+  int64_t page_stride_bytes;
+  int64_t row_bytes;
+  int64_t row_chunks;    // row_bytes / sizeof(Chunk)
+  int slice_shift;       // log2(chunks per column slice)
+  int n_slices;
+  int n_row_tiles;       // private mode: row tiles per sequence
+  int inplace;
+  int budget;
+  const int32_t* seq_lens;
+  const int64_t* src_off;
+  const int64_t* src_ids;
+  const int64_t* dst_off;
+  const int64_t* dst_ids;
+  const int64_t* keep;
+  int64_t keep_stride;
+};
+
+__device__ __forceinline__ int64_t page_of(const int64_t* table, int64_t n_entries, int64_t row,
+                                           int64_t num_pages) {
+  const int64_t blk = row >> kBlockShift;
+  if (row < 0 || blk >= n_entries) return -1;
+  const int64_t p = table[blk];
+  return (p >= 0 && p < num_pages) ? p : -1;
+}
+
+template <typename Chunk>
+__global__ __launch_bounds__(kCopyThreads) void compact_kernel(CompactArgs a) {
+  const int b = blockIdx.y;
+  const int layer = blockIdx.z >> 1;
+  const bool is_v = (blockIdx.z & 1) != 0;
+  char* base = reinterpret_cast<char*>(is_v ? a.v_ptrs[layer] : a.k_ptrs[layer]);
+
+  const int64_t* sbt = a.src_ids + a.src_off[b];
+  const int64_t n_src = a.src_off[b + 1] - a.src_off[b];
+  const int64_t* dbt = a.inplace ? sbt : a.dst_ids + a.dst_off[b];
+  const int64_t n_dst = a.inplace ? n_src : a.dst_off[b + 1] - a.dst_off[b];
+  const int64_t* kp = a.keep + static_cast<int64_t>(b) * a.keep_stride;
+  const int64_t n_tokens = a.seq_lens[b];
+
+  const int slice_w = 1 << a.slice_shift;  // chunks per slice (divides kCopyThreads)
+  const int rows_per_step = kCopyThreads >> a.slice_shift;
+  const int tile_rows = rows_per_step * kCopyUnroll;
+  const int col = threadIdx.x & (slice_w - 1);
+  const int row_lane = threadIdx.x >> a.slice_shift;
+
+  int slice, first_tile, last_tile;
+  if (a.inplace) {
+    slice = blockIdx.x;
+    first_tile = 0;
+    last_tile = (a.budget + tile_rows - 1) / tile_rows;
+  } else {
+    slice = blockIdx.x % a.n_slices;
+    first_tile = blockIdx.x / a.n_slices;
+    last_tile = first_tile + 1;
+  }
+  const int64_t chunk = static_cast<int64_t>(slice) * slice_w + col;
+  const bool col_ok = chunk < a.row_chunks;
+
+  for (int tile = first_tile; tile < last_tile; ++tile) {
+    Chunk v[kCopyUnroll];
+    int64_t dst_off[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = static_cast<int64_t>(tile) * tile_rows + u * rows_per_step + row_lane;
+      dst_off[u] = -1;
+      if (!col_ok || i >= a.budget) continue;
+      const int64_t src_row = kp[i];
+      if (src_row < 0 || src_row >= n_tokens) continue;
+      const int64_t sp = page_of(sbt, n_src, src_row, a.num_pages);
+      const int64_t dp = page_of(dbt, n_dst, i, a.num_pages);
+      if (sp < 0 || dp < 0) continue;
+      const int64_t so = sp * a.page_stride_bytes + (src_row & (kBlockSize - 1)) * a.row_bytes;
+      const int64_t dof = dp * a.page_stride_bytes + (i & (kBlockSize - 1)) * a.row_bytes;
+      if (so == dof) continue;  // row already in place
+      v[u] = *reinterpret_cast<const Chunk*>(base + so + chunk * sizeof(Chunk));
+      dst_off[u] = dof;
+    }
+    if (a.inplace) {
+      // Every load of this tile has returned before any lane stores.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      if (dst_off[u] >= 0)
+        *reinterpret_cast<Chunk*>(base + dst_off[u] + chunk * sizeof(Chunk)) = v[u];
+    }
+  }
+}
+
+__global__ void rewrite_tables_kernel(int n_seq, int nb, const int64_t* __restrict__ src_off,
+                                      const int64_t* __restrict__ src_ids,
+                                      const int64_t* __restrict__ dst_off,
+                                      const int64_t* __restrict__ dst_ids,
+                                      int64_t* __restrict__ new_tables,
+                                      const int64_t* __restrict__ freed_off,
+                                      int64_t* __restrict__ freed_ids) {
+  const int b = blockIdx.x;
+  if (b >= n_seq) return;
+  const int64_t* src = src_ids + src_off[b];
+  const int64_t n_src = src_off[b + 1] - src_off[b];
+  const bool inplace = dst_ids == nullptr;
+  const int64_t* dst = inplace ? src : dst_ids + dst_off[b];
+  const int64_t n_dst = inplace ? n_src : dst_off[b + 1] - dst_off[b];
+  for (int j = threadIdx.x; j < nb; j += blockDim.x)
+    new_tables[static_cast<int64_t>(b) * nb + j] = j < n_dst ? dst[j] : -1;
+  // Released pages in the reference's order: reversed(source pages not reused).
+  const int64_t first_freed = inplace ? (nb < n_src ? nb : n_src) : 0;
+  const int64_t n_freed = n_src - first_freed;
+  const int64_t room = freed_off[b + 1] - freed_off[b];
+  int64_t* out = freed_ids + freed_off[b];
+  for (int64_t k = threadIdx.x; k < n_freed && k < room; k += blockDim.x) out[k] = src[n_src - 1 - k];
+}
+
+__global__ void token_slots_kernel(const int64_t* __restrict__ block_ids, int64_t n_blocks,
+                                   const int64_t* __restrict__ tokens, int64_t n, int block_size,
+                                   int64_t* __restrict__ slots) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t t = tokens[i];
+  if (t < 0) {
+    slots[i] = -1;
+    return;
+  }
+  const int64_t blk = t / block_size;
+  slots[i] = blk < n_blocks ? block_ids[blk] * block_size + t % block_size : -1;
+}
+
+__global__ void expand_ids_kernel(const int64_t* __restrict__ ids, int64_t n, int k,
+                                  int64_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n * k) return;
+  out[i] = ids[i / k] * k + i % k;
+}
+
+// Slot-addressed row copy in 4-byte words: dst_base[dst_slot] <- src_base[src_slot].
+// `gather` reads cache slots into a dense workspace, `!gather` scatters it back.
+__global__ void slot_copy_kernel(const char* __restrict__ src, char* __restrict__ dst,
+                                 const int64_t* __restrict__ slots, int64_t n_slots,
+                                 int64_t num_pages, int64_t page_stride_bytes, int64_t row_bytes,
+                                 int gather) {
+  const int64_t words = row_bytes / 4;
+  const int64_t total = n_slots * words;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = e / words, w = e - r * words;
+    const int64_t slot = slots[r];
+    const int64_t page = slot >> kBlockShift;
+    if (slot < 0 || page >= num_pages) continue;
+    const int64_t cache_off = page * page_stride_bytes + (slot & (kBlockSize - 1)) * row_bytes + w * 4;
+    const int64_t ws_off = r * row_bytes + w * 4;
+    if (gather)
+      *reinterpret_cast<uint32_t*>(dst + ws_off) = *reinterpret_cast<const uint32_t*>(src + cache_off);
+    else
+      *reinterpret_cast<uint32_t*>(dst + cache_off) = *reinterpret_cast<const uint32_t*>(src + ws_off);
+  }
+}
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_layer_ptrs,
+                           const uint64_t* v_layer_ptrs, int64_t num_pages, int64_t page_stride,
+                           int64_t row_elems, int elem_bytes, int n_seq, const int32_t* seq_lens,
+                           const int64_t* src_block_offsets, const int64_t* src_block_ids,
+                           const int64_t* dst_block_offsets, const int64_t* dst_block_ids,
+                           const int64_t* keep, int64_t keep_stride, int budget) {
+  if (n_layers <= 0 || n_layers > 32767 || n_seq <= 0 || n_seq > 65535)
+    return fail(KVC_EINVAL, "kvc_compact: bad layer or sequence count");
+  if (elem_bytes != 2) return fail(KVC_EINVAL, "kvc_compact: elem_bytes must be 2");
+  if (row_elems <= 0 || budget <= 0 || keep_stride < budget || num_pages <= 0)
+    return fail(KVC_EINVAL, "kvc_compact: bad sizes");
+  if (page_stride < row_elems * kBlockSize)
+    return fail(KVC_EINVAL, "kvc_compact: page stride smaller than a page");
+  if (!k_layer_ptrs || !v_layer_ptrs || !seq_lens || !src_block_offsets || !src_block_ids || !keep)
+    return fail(KVC_EINVAL, "kvc_compact: null pointer");
+  const bool inplace = dst_block_ids == nullptr;
+  if (!inplace && !dst_block_offsets)
+    return fail(KVC_EINVAL, "kvc_compact: destination offsets missing");
+
+  CompactArgs ca;
+  ca.k_ptrs = k_layer_ptrs;
+  ca.v_ptrs = v_layer_ptrs;
+  ca.num_pages = num_pages;
+  ca.page_stride_bytes = page_stride * elem_bytes;
+  ca.row_bytes = row_elems * elem_bytes;
+  ca.inplace = inplace ? 1 : 0;
+  ca.budget = budget;
+  ca.seq_lens = seq_lens;
+  ca.src_off = src_block_offsets;
+  ca.src_ids = src_block_ids;
+  ca.dst_off = dst_block_offsets;
+  ca.dst_ids = dst_block_ids;
+  ca.keep = keep;
+  ca.keep_stride = keep_stride;
+
+  // Widest word that divides both the row and the page stride.
+  int word = 16;
+  while (word > 2 && ((ca.row_bytes % word) != 0 || (ca.page_stride_bytes % word) != 0)) word >>= 1;
+  ca.row_chunks = ca.row_bytes / word;
+
+  // Column slice: whole rows (up to 256 words) in private mode; 256-byte
+  // slices in place, so enough independent workgroups fill the chip.
+  int64_t target = inplace ? (256 / word) : ca.row_chunks;
+  if (target > kCopyThreads) target = kCopyThreads;
+  int shift = 0;
+  while ((1 << shift) < target) ++shift;
+  ca.slice_shift = shift;
+  ca.n_slices = static_cast<int>(ceil_div(ca.row_chunks, int64_t(1) << shift));
+  const int rows_per_step = kCopyThreads >> shift;
+  const int tile_rows = rows_per_step * kCopyUnroll;
+  ca.n_row_tiles = static_cast<int>(ceil_div(budget, tile_rows));
+  const int64_t gx = inplace ? ca.n_slices : static_cast<int64_t>(ca.n_slices) * ca.n_row_tiles;
+  if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n_seq),
+            static_cast<unsigned>(2 * n_layers));
+  hipStream_t st = as_stream(stream);
+  switch (word) {
+    case 16: compact_kernel<uint4><<<grid, kCopyThreads, 0, st>>>(ca); break;
+    case 8: compact_kernel<uint2><<<grid, kCopyThreads, 0, st>>>(ca); break;
+    case 4: compact_kernel<uint32_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+    default: compact_kernel<uint16_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+  }
+  return launch_status("kvc_compact");
+}
+
+extern "C" int kvc_rewrite_block_tables(kvc_stream_t stream, int n_seq, int budget,
+                                        const int64_t* src_block_offsets,
+                                        const int64_t* src_block_ids,
+                                        const int64_t* dst_block_offsets,
+                                        const int64_t* dst_block_ids, int64_t* new_tables,
+                                        const int64_t* freed_offsets, int64_t* freed_ids) {
+  if (n_seq <= 0 || budget <= 0) return fail(KVC_EINVAL, "kvc_rewrite_block_tables: bad sizes");
+  if (!src_block_offsets || !src_block_ids || !new_tables || !freed_offsets || !freed_ids)
+    return fail(KVC_EINVAL, "kvc_rewrite_block_tables: null pointer");
+  if (dst_block_ids && !dst_block_offsets)
+    return fail(KVC_EINVAL, "kvc_rewrite_block_tables: destination offsets missing");
+  const int nb = static_cast<int>(ceil_div(budget, kBlockSize));
+  rewrite_tables_kernel<<<n_seq, 256, 0, as_stream(stream)>>>(
+      n_seq, nb, src_block_offsets, src_block_ids, dst_block_offsets, dst_block_ids, new_tables,
+      freed_offsets, freed_ids);
+  return launch_status("kvc_rewrite_block_tables");
+}
+
+extern "C" int kvc_token_slots(kvc_stream_t stream, const int64_t* block_ids, int64_t n_blocks,
+                               const int64_t* token_indices, int64_t n_tokens, int block_size,
+                               int64_t* slots) {
+  if (n_tokens < 0 || n_blocks < 0 || block_size <= 0)
+    return fail(KVC_EINVAL, "kvc_token_slots: bad sizes");
+  if (n_tokens == 0) return 0;
+  if (!block_ids || !token_indices || !slots) return fail(KVC_EINVAL, "kvc_token_slots: null pointer");
+  token_slots_kernel<<<static_cast<unsigned>(ceil_div(n_tokens, 256)), 256, 0, as_stream(stream)>>>(
+      block_ids, n_blocks, token_indices, n_tokens, block_size, slots);
+  return launch_status("kvc_token_slots");
+}
+
+extern "C" int kvc_expand_block_ids(kvc_stream_t stream, const int64_t* ids, int64_t n_ids, int k,
+                                    int64_t* out) {
+  if (n_ids < 0 || k <= 0) return fail(KVC_EINVAL, "kvc_expand_block_ids: bad sizes");
+  if (n_ids == 0) return 0;
+  if (!ids || !out) return fail(KVC_EINVAL, "kvc_expand_block_ids: null pointer");
+  const int64_t total = n_ids * k;
+  expand_ids_kernel<<<static_cast<unsigned>(ceil_div(total, 256)), 256, 0, as_stream(stream)>>>(
+      ids, n_ids, k, out);
+  return launch_status("kvc_expand_block_ids");
+}
+
+extern "C" int kvc_materialize_slots(kvc_stream_t stream, void* k_cache, void* v_cache,
+                                     int64_t num_pages, int64_t page_stride, int64_t row_elems,
+                                     int elem_bytes, const int64_t* src_slots,
+                                     const int64_t* dst_slots, int64_t n_slots, void* k_ws,
+                                     void* v_ws) {
+  if (elem_bytes != 2 || row_elems <= 0 || num_pages <= 0 || n_slots < 0)
+    return fail(KVC_EINVAL, "kvc_materialize_slots: bad sizes");
+  if (page_stride < row_elems * kBlockSize)
+    return fail(KVC_EINVAL, "kvc_materialize_slots: page stride smaller than a page");
+  const int64_t row_bytes = row_elems * elem_bytes;
+  const int64_t ps_bytes = page_stride * elem_bytes;
+  if (row_bytes % 4 != 0 || ps_bytes % 4 != 0)
+    return fail(KVC_EINVAL, "kvc_materialize_slots: rows and pages must be 4-byte multiples");
+  if (n_slots == 0) return 0;
+  if (!k_cache || !v_cache || !src_slots || !dst_slots || !k_ws || !v_ws)
+    return fail(KVC_EINVAL, "kvc_materialize_slots: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int64_t total = n_slots * (row_bytes / 4);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(total, 256) < 65536 ? ceil_div(total, 256) : 65536);
+  slot_copy_kernel<<<blocks, 256, 0, st>>>(static_cast<const char*>(k_cache),
+                                           static_cast<char*>(k_ws), src_slots, n_slots, num_pages,
+                                           ps_bytes, row_bytes, 1);
+  slot_copy_kernel<<<blocks, 256, 0, st>>>(static_cast<const char*>(v_cache),
+                                           static_cast<char*>(v_ws), src_slots, n_slots, num_pages,
+                                           ps_bytes, row_bytes, 1);
+  slot_copy_kernel<<<blocks, 256, 0, st>>>(static_cast<const char*>(k_ws),
+                                           static_cast<char*>(k_cache), dst_slots, n_slots,
+                                           num_pages, ps_bytes, row_bytes, 0);
+  slot_copy_kernel<<<blocks, 256, 0, st>>>(static_cast<const char*>(v_ws),
+                                           static_cast<char*>(v_cache), dst_slots, n_slots,
+                                           num_pages, ps_bytes, row_bytes, 0);
+  return launch_status("kvc_materialize_slots");
+}

@@ -1,0 +1,696 @@
+// TriAttention paged-K scoring on CDNA4.
+//
+// Kernels:
+//   mean_phases_kernel      phase table cos/sin means per (sequence, layer, freq)
+//   shift_phases_kernel     the reference device path's angle-addition table
+//   fold_weights_kernel     folds calibration stats and phases into per-lane weights
+//   score_paged_kernel      reads K once through the block table, writes raw scores
+//                           and per-tile float64 partial sums for the head statistics
+//   head_stats_kernel       combines the partials into population mean / variance
+//   aggregate_kernel        z-normalise, max over heads, combine across layers
+//
+// Score algebra (tri/scoring.py:66-119).  With a = sqrt(freq_scale_sq), phase
+// means c_f, s_f and extra = q_abs - |q_mean|, the score of a post-RoPE key is
+//   sum_f a[(qr kr + qi ki) c - (qi kr - qr ki) s] + a*extra*|k_f|  + q_pass.k_pass
+// = sum_f kr*W1 + ki*W2 + |k_f|*W3                                  + q_pass.k_pass
+// with W1 = a(qr c - qi s), W2 = a(qi c + qr s), W3 = a*extra.  The fold happens
+// once per (sequence, layer) so the per-token work is three FMAs per frequency
+// per query head, and K is read once per KV head for the whole GQA group.
+//
+// Lane layout of score_paged_kernel.  A "unit" is two 16-byte chunks of one
+// head row: for a rotary unit the 8 real and the 8 imaginary components of 8
+// frequencies (half style: dims [8u,8u+8) and [F+8u,F+8u+8); interleaved:
+// dims [16u,16u+16)), for a pass unit 16 consecutive unrotated dims.  The
+// units of one head row form a lane group of `group` lanes (a power of two);
+// a wave holds 64/group groups, each bound to a fixed KV head, so the weights
+// stay in registers and every wave load instruction covers whole 128-byte
+// lines of consecutive head rows.  Partial dot products are summed across the
+// group with DPP, and lane g of the group writes query head g of its KV head.
+
+#include <math.h>
+#include <stdarg.h>
+
+#include "kvc_common.h"
+
+namespace kvc {
+namespace {
+
+constexpr int kScoreTile = 256;     // tokens per scoring workgroup
+constexpr int kScoreThreads = 256;  // 4 waves
+constexpr int kUnroll = 4;          // token iterations with loads in flight
+
+struct ScoreShape {
+  int n_layers, kv_heads, head_dim, rotary_dim, qpk;
+  int freq, pass, units_rot, units, group_shift;
+  int n_seq, max_tiles;
+};
+
+bool make_shape(ScoreShape* s, int n_layers, int kv_heads, int head_dim, int rotary_dim, int qpk,
+                int n_seq, int max_seq_len) {
+  if (n_layers <= 0 || kv_heads <= 0 || head_dim <= 0 || qpk <= 0 || qpk > 8 || n_seq <= 0 ||
+      max_seq_len < 0)
+    return false;
+  if (rotary_dim <= 0 || rotary_dim > head_dim || rotary_dim % 16 != 0) return false;
+  const int freq = rotary_dim / 2;
+  const int pass = head_dim - rotary_dim;
+  if (pass % 16 != 0) return false;
+  s->n_layers = n_layers;
+  s->kv_heads = kv_heads;
+  s->head_dim = head_dim;
+  s->rotary_dim = rotary_dim;
+  s->qpk = qpk;
+  s->freq = freq;
+  s->pass = pass;
+  s->units_rot = freq / 8;
+  s->units = freq / 8 + pass / 16;
+  int need = s->units > qpk ? s->units : qpk;
+  int shift = 0;
+  while ((1 << shift) < need) ++shift;
+  if (shift > 6) return false;  // one head row must fit in a wave
+  s->group_shift = shift;
+  // A workgroup covers every KV head of a token; groups beyond the last whole
+  // token slot stay idle.
+  const int groups_per_wg = (kScoreThreads / 64) * (64 >> shift);
+  if (groups_per_wg < kv_heads) return false;
+  s->n_seq = n_seq;
+  s->max_tiles = static_cast<int>(ceil_div(max_seq_len, kScoreTile));
+  return true;
+}
+
+size_t weights_floats(const ScoreShape& s) {
+  return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.units * 3 * s.qpk * 8;
+}
+size_t weights_bytes_aligned(const ScoreShape& s) {
+  return (weights_floats(s) * sizeof(float) + 255) / 256 * 256;
+}
+size_t partial_count(const ScoreShape& s) {
+  return static_cast<size_t>(s.n_layers) * s.n_seq * (s.max_tiles > 0 ? s.max_tiles : 1) *
+         s.kv_heads * s.qpk;
+}
+size_t workspace_bytes(const ScoreShape& s) {
+  return weights_bytes_aligned(s) + partial_count(s) * 2 * sizeof(double);
+}
+
+// ------------------------------------------------------------- phase tables --
+
+// One thread per (sequence, layer, frequency).  The phase argument is formed
+// exactly as the torch path does in float32, (offset + round_start) * omega,
+// and its cosine/sine are evaluated in double and rounded once, so the table
+// agrees with a correctly rounded float32 evaluation.  The mean is a
+// sequential float32 sum in offset order divided by the offset count.
+__global__ void mean_phases_kernel(int n_seq, int n_layers, int n_freq,
+                                   const int64_t* __restrict__ round_starts,
+                                   const float* __restrict__ offsets, int n_offsets,
+                                   const float* __restrict__ omega, float* __restrict__ phase_cos,
+                                   float* __restrict__ phase_sin) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t per_seq = static_cast<int64_t>(n_layers) * n_freq;
+  if (idx >= per_seq * n_seq) return;
+  const int64_t b = idx / per_seq;
+  const int64_t lf = idx - b * per_seq;
+  const float rs = static_cast<float>(round_starts[b]);
+  const float w = omega[lf];
+  float c = 0.0f, s = 0.0f;
+  for (int o = 0; o < n_offsets; ++o) {
+    const float x = __fmul_rn(__fadd_rn(offsets[o], rs), w);
+    c = __fadd_rn(c, static_cast<float>(cos(static_cast<double>(x))));
+    s = __fadd_rn(s, static_cast<float>(sin(static_cast<double>(x))));
+  }
+  const float n = static_cast<float>(n_offsets);
+  phase_cos[idx] = __fdiv_rn(c, n);
+  phase_sin[idx] = __fdiv_rn(s, n);
+}
+
+// Angle addition from precomputed offset means (tri/kernels.py:70-82).
+__global__ void shift_phases_kernel(int n_values, float round_start,
+                                    const float* __restrict__ omega,
+                                    const float* __restrict__ offset_cos,
+                                    const float* __restrict__ offset_sin,
+                                    float* __restrict__ phase_cos, float* __restrict__ phase_sin) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_values) return;
+  const float x = __fmul_rn(round_start, omega[i]);
+  const float rc = static_cast<float>(cos(static_cast<double>(x)));
+  const float rsn = static_cast<float>(sin(static_cast<double>(x)));
+  const float oc = offset_cos[i], os = offset_sin[i];
+  phase_cos[i] = __fsub_rn(__fmul_rn(rc, oc), __fmul_rn(rsn, os));
+  phase_sin[i] = __fadd_rn(__fmul_rn(rsn, oc), __fmul_rn(rc, os));
+}
+
+// ------------------------------------------------------------- weight fold --
+
+struct FoldArgs {
+  int n_seq, n_layers, kv_heads, qpk, freq, pass, units_rot, units, rotary_dim;
+  const float* q_real;
+  const float* q_imag;
+  const float* scale;
+  const float* extra;
+  const float* q_pass;
+  const float* phase_cos;
+  const float* phase_sin;
+  int64_t phase_seq_stride;
+  float* weights;  // [n_seq][n_layers][kv_heads][units][3][qpk][8]
+};
+
+__global__ void fold_weights_kernel(FoldArgs a) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * a.units;
+  if (idx >= total) return;
+  const int unit = static_cast<int>(idx % a.units);
+  int64_t r = idx / a.units;
+  const int head = static_cast<int>(r % a.kv_heads);
+  r /= a.kv_heads;
+  const int layer = static_cast<int>(r % a.n_layers);
+  const int b = static_cast<int>(r / a.n_layers);
+  float* out = a.weights + idx * 3 * a.qpk * 8;
+  const int64_t stat_row = (static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk;
+  if (unit < a.units_rot) {
+    const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
+    const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
+    for (int g = 0; g < a.qpk; ++g) {
+      const int64_t base = (stat_row + g) * a.freq;
+      for (int j = 0; j < 8; ++j) {
+        const int f = unit * 8 + j;
+        const float qr = a.q_real[base + f], qi = a.q_imag[base + f];
+        const float sc = a.scale[base + f], ex = a.extra[base + f];
+        const float c = pc[f], s = ps[f];
+        out[(0 * a.qpk + g) * 8 + j] = sc * (qr * c - qi * s);
+        out[(1 * a.qpk + g) * 8 + j] = sc * (qi * c + qr * s);
+        out[(2 * a.qpk + g) * 8 + j] = sc * ex;
+      }
+    }
+  } else {
+    const int u = unit - a.units_rot;
+    for (int g = 0; g < a.qpk; ++g) {
+      const float* qp = a.q_pass + (stat_row + g) * a.pass + u * 16;
+      for (int j = 0; j < 8; ++j) {
+        out[(0 * a.qpk + g) * 8 + j] = qp[j];
+        out[(1 * a.qpk + g) * 8 + j] = qp[8 + j];
+        out[(2 * a.qpk + g) * 8 + j] = 0.0f;
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- scoring --
+
+struct ScoreArgs {
+  const uint64_t* k_layer_ptrs;
+  int64_t num_pages, page_stride;
+  int kv_heads, head_dim, rotary_dim, freq;
+  int units_rot, units, group_shift;
+  int n_seq, max_tiles, n_layers;
+  const int32_t* seq_lens;
+  const int64_t* token_offsets;
+  const int64_t* block_offsets;
+  const int64_t* block_ids;
+  const float* weights;
+  float* raw;
+  int64_t raw_layer_stride, raw_token_stride, raw_head_stride;
+  double* partials;  // [n_layers][n_seq][max_tiles][kv_heads*QPK][2]
+};
+
+template <typename Tag, int QPK, bool INTERLEAVED>
+__global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a) {
+  const int layer = blockIdx.z;
+  const int b = blockIdx.y;
+  const int tile = blockIdx.x;
+  const int n = a.seq_lens[b];
+  const int t0 = tile * kScoreTile;
+  if (t0 >= n) return;  // whole workgroup leaves together
+  const int t1 = min(n, t0 + kScoreTile);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int gsize = 1 << a.group_shift;
+  const int groups_per_wave = 64 >> a.group_shift;
+  const int unit = lane & (gsize - 1);
+  const int gid = wave * groups_per_wave + (lane >> a.group_shift);
+  const int n_groups = (kScoreThreads / 64) * groups_per_wave;
+  const int head = gid % a.kv_heads;
+  const int tslot = gid / a.kv_heads;
+  const int tpi = n_groups / a.kv_heads;  // tokens per iteration of the workgroup
+  const bool active = unit < a.units && tslot < tpi;
+  const bool rotary = unit < a.units_rot;
+
+  // Per-lane folded weights for (sequence, layer, head, unit).
+  float w1[QPK][8], w2[QPK][8], w3[QPK][8];
+  if (active) {
+    const float4* wp = reinterpret_cast<const float4*>(
+        a.weights +
+        ((((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * a.units + unit) *
+         3 * QPK * 8));
+#pragma unroll
+    for (int g = 0; g < QPK; ++g) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 v1 = wp[(0 * QPK + g) * 2 + h];
+        const float4 v2 = wp[(1 * QPK + g) * 2 + h];
+        const float4 v3 = wp[(2 * QPK + g) * 2 + h];
+        w1[g][4 * h + 0] = v1.x; w1[g][4 * h + 1] = v1.y; w1[g][4 * h + 2] = v1.z; w1[g][4 * h + 3] = v1.w;
+        w2[g][4 * h + 0] = v2.x; w2[g][4 * h + 1] = v2.y; w2[g][4 * h + 2] = v2.z; w2[g][4 * h + 3] = v2.w;
+        w3[g][4 * h + 0] = v3.x; w3[g][4 * h + 1] = v3.y; w3[g][4 * h + 2] = v3.z; w3[g][4 * h + 3] = v3.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < QPK; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w1[g][j] = w2[g][j] = w3[g][j] = 0.0f;
+  }
+
+  // Element offsets of the lane's two chunks inside the head row.
+  int d1, d2;
+  if (rotary) {
+    if (INTERLEAVED) {
+      d1 = 16 * unit;
+      d2 = d1 + 8;
+    } else {
+      d1 = 8 * unit;
+      d2 = a.freq + 8 * unit;
+    }
+  } else {
+    d1 = a.rotary_dim + 16 * (unit - a.units_rot);
+    d2 = d1 + 8;
+  }
+
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k_layer_ptrs[layer]);
+  const int64_t* bt = a.block_ids + a.block_offsets[b];
+  const int64_t n_blocks = a.block_offsets[b + 1] - a.block_offsets[b];
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * a.head_dim;
+  const int64_t head_off = static_cast<int64_t>(head) * a.head_dim;
+  const int64_t tok_base = a.token_offsets[b];
+  float* raw_out = a.raw + layer * a.raw_layer_stride;
+  const bool writer = unit < QPK && tslot < tpi;
+  const int q_head = head * QPK + unit;
+
+  double sum = 0.0, sumsq = 0.0;
+  const int iters = (t1 - t0 + tpi - 1) / tpi;
+  for (int k0 = 0; k0 < iters; k0 += kUnroll) {
+    uint4 ca[kUnroll], cb[kUnroll];
+    bool valid[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int t = t0 + tslot + (k0 + u) * tpi;
+      valid[u] = (k0 + u < iters) && (t < t1);
+      ca[u] = make_uint4(0, 0, 0, 0);
+      cb[u] = make_uint4(0, 0, 0, 0);
+      const int64_t blk = t >> kBlockShift;
+      if (valid[u] && active && blk < n_blocks) {
+        const int64_t page = bt[blk];
+        if (page >= 0 && page < a.num_pages) {
+          const uint16_t* row = kbase + page * a.page_stride +
+                                static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
+          ca[u] = *reinterpret_cast<const uint4*>(row + d1);
+          cb[u] = *reinterpret_cast<const uint4*>(row + d2);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      float x1[8], x2[8], x3[8];
+      const uint32_t wa[4] = {ca[u].x, ca[u].y, ca[u].z, ca[u].w};
+      const uint32_t wb[4] = {cb[u].x, cb[u].y, cb[u].z, cb[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (INTERLEAVED) {
+          // rotary: dword j of chunk a holds (re_j, im_j); of chunk b (re_{4+j}, im_{4+j})
+          // pass: chunk a holds dims 0..7, chunk b dims 8..15 of the unit
+          const float alo = Unpack<Tag>::lo(wa[j]), ahi = Unpack<Tag>::hi(wa[j]);
+          const float blo = Unpack<Tag>::lo(wb[j]), bhi = Unpack<Tag>::hi(wb[j]);
+          if (rotary) {
+            x1[j] = alo; x2[j] = ahi; x1[4 + j] = blo; x2[4 + j] = bhi;
+          } else {
+            x1[2 * j] = alo; x1[2 * j + 1] = ahi; x2[2 * j] = blo; x2[2 * j + 1] = bhi;
+          }
+        } else {
+          x1[2 * j] = Unpack<Tag>::lo(wa[j]);
+          x1[2 * j + 1] = Unpack<Tag>::hi(wa[j]);
+          x2[2 * j] = Unpack<Tag>::lo(wb[j]);
+          x2[2 * j + 1] = Unpack<Tag>::hi(wb[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float m = sqrtf(fmaf(x2[j], x2[j], x1[j] * x1[j]));
+        x3[j] = rotary ? m : 0.0f;
+      }
+      float acc[QPK];
+#pragma unroll
+      for (int g = 0; g < QPK; ++g) {
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          v = fmaf(w1[g][j], x1[j], v);
+          v = fmaf(w2[g][j], x2[j], v);
+          v = fmaf(w3[g][j], x3[j], v);
+        }
+        acc[g] = group_sum(v, gsize);
+      }
+      float mine = acc[0];
+#pragma unroll
+      for (int g = 1; g < QPK; ++g) mine = (unit == g) ? acc[g] : mine;
+      if (valid[u] && writer) {
+        const int t = t0 + tslot + (k0 + u) * tpi;
+        raw_out[(tok_base + t) * a.raw_token_stride + q_head * a.raw_head_stride] = mine;
+        const double dv = static_cast<double>(mine);
+        sum += dv;
+        sumsq = fma(dv, dv, sumsq);
+      }
+    }
+  }
+
+  // Combine the per-lane partial sums of each query head in a fixed order.
+  __shared__ double red[2][kScoreThreads];
+  red[0][threadIdx.x] = sum;
+  red[1][threadIdx.x] = sumsq;
+  __syncthreads();
+  const int n_heads = a.kv_heads * QPK;
+  for (int q = threadIdx.x; q < n_heads; q += kScoreThreads) {
+    const int h = q / QPK, g = q - h * QPK;
+    double s0 = 0.0, s1 = 0.0;
+    for (int slot = 0; slot < tpi; ++slot) {
+      const int gg = slot * a.kv_heads + h;  // group bound to head h, token slot `slot`
+      const int th = (gg / groups_per_wave) * 64 + (gg % groups_per_wave) * gsize + g;
+      s0 += red[0][th];
+      s1 += red[1][th];
+    }
+    double* dst = a.partials +
+                  (((static_cast<int64_t>(layer) * a.n_seq + b) * a.max_tiles + tile) * n_heads + q) * 2;
+    dst[0] = s0;
+    dst[1] = s1;
+  }
+}
+
+// --------------------------------------------------------------- head stats --
+
+__global__ void head_stats_kernel(int n_layers, int n_seq, int n_heads, int max_tiles,
+                                  const int32_t* __restrict__ seq_lens,
+                                  const double* __restrict__ partials, float* __restrict__ mean,
+                                  float* __restrict__ var) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(n_layers) * n_seq * n_heads) return;
+  const int q = static_cast<int>(idx % n_heads);
+  const int64_t ls = idx / n_heads;  // layer * n_seq + b
+  const int b = static_cast<int>(ls % n_seq);
+  const int n = seq_lens[b];
+  const int tiles = static_cast<int>((n + kScoreTile - 1) / kScoreTile);
+  double s0 = 0.0, s1 = 0.0;
+  for (int t = 0; t < tiles; ++t) {
+    const double* p = partials + ((ls * max_tiles + t) * n_heads + q) * 2;
+    s0 += p[0];
+    s1 += p[1];
+  }
+  const double inv_n = 1.0 / static_cast<double>(n);
+  const double m = s0 * inv_n;
+  double v = s1 * inv_n - m * m;
+  if (v < 0.0) v = 0.0;
+  mean[idx] = static_cast<float>(m);
+  var[idx] = static_cast<float>(v);
+}
+
+// ---------------------------------------------------------------- aggregate --
+
+constexpr int kAggThreads = 256;
+constexpr int kAggMaxStats = 2048;  // layers * heads staged in LDS
+
+struct AggArgs {
+  int n_layers, n_heads, n_seq, layer_mode;
+  unsigned flags;
+  const int32_t* seq_lens;
+  const int64_t* token_offsets;
+  const float* raw;
+  int64_t raw_layer_stride, raw_token_stride, raw_head_stride;
+  const float* mean;
+  const float* var;
+  int64_t stats_layer_stride, stats_seq_stride;
+  float* agg;
+};
+
+__global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
+  __shared__ float s_mean[kAggMaxStats];
+  __shared__ float s_scale[kAggMaxStats];
+  const int b = blockIdx.y;
+  const int n = a.seq_lens[b];
+  const int t = blockIdx.x * kAggThreads + threadIdx.x;
+  if (static_cast<int64_t>(blockIdx.x) * kAggThreads >= n) return;
+  const int n_stats = a.n_layers * a.n_heads;
+  const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
+  for (int i = threadIdx.x; i < n_stats; i += kAggThreads) {
+    const int l = i / a.n_heads, h = i - l * a.n_heads;
+    const int64_t si = l * a.stats_layer_stride + b * a.stats_seq_stride + h;
+    const float v = fmaxf(a.var[si], 1e-6f);
+    s_mean[i] = a.mean[si];
+    s_scale[i] = rsqrt_form ? rsqrtf(v) : sqrtf(v);
+  }
+  __syncthreads();
+  if (t >= n) return;
+  const int64_t tok = a.token_offsets[b] + t;
+  float total = 0.0f;
+  for (int l = 0; l < a.n_layers; ++l) {
+    const float* row = a.raw + l * a.raw_layer_stride + tok * a.raw_token_stride;
+    float best = -INFINITY;
+    for (int h = 0; h < a.n_heads; ++h) {
+      const float s = row[h * a.raw_head_stride];
+      const int i = l * a.n_heads + h;
+      const float z = rsqrt_form ? (s - s_mean[i]) * s_scale[i] : (s - s_mean[i]) / s_scale[i];
+      best = (h == 0) ? z : max_nan(best, z);
+    }
+    if (l == 0) {
+      if (a.flags & KVC_AGG_ACCUMULATE) {
+        const float prev = a.agg[tok];
+        total = (a.layer_mode == KVC_LAYER_MEAN) ? prev + best : max_nan(prev, best);
+      } else {
+        total = best;
+      }
+    } else {
+      total = (a.layer_mode == KVC_LAYER_MEAN) ? total + best : max_nan(total, best);
+    }
+  }
+  if (a.flags & KVC_AGG_FINALIZE) {
+    if (a.layer_mode == KVC_LAYER_MEAN) total = total / static_cast<float>(a.n_layers);
+    if (total != total) total = -INFINITY;
+    else if (total == INFINITY) total = 1e30f;
+  }
+  a.agg[tok] = total;
+}
+
+template <typename Tag, bool IL>
+using ScoreKernelFn = void (*)(ScoreArgs);
+
+template <typename Tag, bool IL>
+ScoreKernelFn<Tag, IL> pick_score_kernel(int qpk) {
+  switch (qpk) {
+    case 1: return score_paged_kernel<Tag, 1, IL>;
+    case 2: return score_paged_kernel<Tag, 2, IL>;
+    case 3: return score_paged_kernel<Tag, 3, IL>;
+    case 4: return score_paged_kernel<Tag, 4, IL>;
+    case 5: return score_paged_kernel<Tag, 5, IL>;
+    case 6: return score_paged_kernel<Tag, 6, IL>;
+    case 7: return score_paged_kernel<Tag, 7, IL>;
+    case 8: return score_paged_kernel<Tag, 8, IL>;
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+}  // namespace kvc
+
+using namespace kvc;
+
+extern "C" int kvc_mean_phases(kvc_stream_t stream, int n_seq, int n_layers, int n_freq,
+                               const int64_t* round_starts, const float* offsets, int n_offsets,
+                               const float* omega, float* phase_cos, float* phase_sin) {
+  if (n_seq <= 0 || n_layers <= 0 || n_freq <= 0 || n_offsets <= 0)
+    return fail(KVC_EINVAL, "kvc_mean_phases: sizes must be positive");
+  if (!round_starts || !offsets || !omega || !phase_cos || !phase_sin)
+    return fail(KVC_EINVAL, "kvc_mean_phases: null pointer");
+  const int64_t total = static_cast<int64_t>(n_seq) * n_layers * n_freq;
+  mean_phases_kernel<<<static_cast<unsigned>(ceil_div(total, 256)), 256, 0, as_stream(stream)>>>(
+      n_seq, n_layers, n_freq, round_starts, offsets, n_offsets, omega, phase_cos, phase_sin);
+  return launch_status("kvc_mean_phases");
+}
+
+extern "C" int kvc_shift_mean_phases(kvc_stream_t stream, int n_values, int64_t round_start,
+                                     const float* omega, const float* offset_cos_mean,
+                                     const float* offset_sin_mean, float* phase_cos,
+                                     float* phase_sin) {
+  if (n_values <= 0) return fail(KVC_EINVAL, "kvc_shift_mean_phases: n_values must be positive");
+  if (!omega || !offset_cos_mean || !offset_sin_mean || !phase_cos || !phase_sin)
+    return fail(KVC_EINVAL, "kvc_shift_mean_phases: null pointer");
+  shift_phases_kernel<<<static_cast<unsigned>(ceil_div(n_values, 256)), 256, 0,
+                        as_stream(stream)>>>(n_values, static_cast<float>(round_start), omega,
+                                             offset_cos_mean, offset_sin_mean, phase_cos,
+                                             phase_sin);
+  return launch_status("kvc_shift_mean_phases");
+}
+
+extern "C" size_t kvc_score_workspace_bytes(int n_layers, int kv_heads, int head_dim,
+                                            int rotary_dim, int qpk, int n_seq, int max_seq_len) {
+  ScoreShape s;
+  if (!make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len)) return 0;
+  return workspace_bytes(s);
+}
+
+extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
+                               const uint64_t* k_layer_ptrs, int64_t num_pages,
+                               int64_t page_stride, int kv_heads, int head_dim, int rotary_dim,
+                               int qpk, int rope_style, int n_seq, int max_seq_len,
+                               const int32_t* seq_lens, const int64_t* token_offsets,
+                               const int64_t* block_offsets, const int64_t* block_ids,
+                               const float* q_real, const float* q_imag, const float* freq_scale,
+                               const float* extra_coef, const float* q_pass,
+                               const float* phase_cos, const float* phase_sin,
+                               int64_t phase_seq_stride, float* raw, int64_t raw_layer_stride,
+                               int64_t raw_token_stride, int64_t raw_head_stride, void* workspace,
+                               size_t workspace_bytes_given) {
+  ScoreShape s;
+  if (!make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len))
+    return fail(KVC_EINVAL,
+                "kvc_score_paged: unsupported shape (layers=%d kv_heads=%d head_dim=%d "
+                "rotary_dim=%d qpk=%d n_seq=%d); rotary_dim and head_dim-rotary_dim must be "
+                "multiples of 16, qpk <= 8",
+                n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq);
+  if (dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16)
+    return fail(KVC_EINVAL, "kvc_score_paged: dtype must be bf16 or fp16");
+  if (rope_style != KVC_ROPE_HALF && rope_style != KVC_ROPE_INTERLEAVED)
+    return fail(KVC_EINVAL, "kvc_score_paged: unknown rope style %d", rope_style);
+  if (page_stride < static_cast<int64_t>(kBlockSize) * kv_heads * head_dim || num_pages <= 0)
+    return fail(KVC_EINVAL, "kvc_score_paged: page stride smaller than a page");
+  if (!k_layer_ptrs || !seq_lens || !token_offsets || !block_offsets || !block_ids || !q_real ||
+      !q_imag || !freq_scale || !extra_coef || !phase_cos || !phase_sin || !raw || !workspace)
+    return fail(KVC_EINVAL, "kvc_score_paged: null pointer");
+  if (s.pass > 0 && !q_pass)
+    return fail(KVC_EINVAL, "kvc_score_paged: partial RoPE requires q_pass");
+  if (workspace_bytes_given < workspace_bytes(s))
+    return fail(KVC_EINVAL, "kvc_score_paged: workspace too small (%zu < %zu)",
+                workspace_bytes_given, workspace_bytes(s));
+  if (s.max_tiles == 0) return 0;
+  hipStream_t st = as_stream(stream);
+
+  float* weights = static_cast<float*>(workspace);
+  double* partials =
+      reinterpret_cast<double*>(static_cast<char*>(workspace) + weights_bytes_aligned(s));
+
+  FoldArgs fa;
+  fa.n_seq = n_seq;
+  fa.n_layers = n_layers;
+  fa.kv_heads = kv_heads;
+  fa.qpk = qpk;
+  fa.freq = s.freq;
+  fa.pass = s.pass;
+  fa.units_rot = s.units_rot;
+  fa.units = s.units;
+  fa.rotary_dim = rotary_dim;
+  fa.q_real = q_real;
+  fa.q_imag = q_imag;
+  fa.scale = freq_scale;
+  fa.extra = extra_coef;
+  fa.q_pass = q_pass;
+  fa.phase_cos = phase_cos;
+  fa.phase_sin = phase_sin;
+  fa.phase_seq_stride = phase_seq_stride;
+  fa.weights = weights;
+  const int64_t fold_threads = static_cast<int64_t>(n_seq) * n_layers * kv_heads * s.units;
+  fold_weights_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 64)), 64, 0, st>>>(fa);
+  if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
+
+  ScoreArgs sa;
+  sa.k_layer_ptrs = k_layer_ptrs;
+  sa.num_pages = num_pages;
+  sa.page_stride = page_stride;
+  sa.kv_heads = kv_heads;
+  sa.head_dim = head_dim;
+  sa.rotary_dim = rotary_dim;
+  sa.freq = s.freq;
+  sa.units_rot = s.units_rot;
+  sa.units = s.units;
+  sa.group_shift = s.group_shift;
+  sa.n_seq = n_seq;
+  sa.max_tiles = s.max_tiles;
+  sa.n_layers = n_layers;
+  sa.seq_lens = seq_lens;
+  sa.token_offsets = token_offsets;
+  sa.block_offsets = block_offsets;
+  sa.block_ids = block_ids;
+  sa.weights = weights;
+  sa.raw = raw;
+  sa.raw_layer_stride = raw_layer_stride;
+  sa.raw_token_stride = raw_token_stride;
+  sa.raw_head_stride = raw_head_stride;
+  sa.partials = partials;
+
+  void (*kern)(ScoreArgs) = nullptr;
+  const bool il = rope_style == KVC_ROPE_INTERLEAVED;
+  if (dtype == KVC_DTYPE_BF16)
+    kern = il ? pick_score_kernel<Bf16Tag, true>(qpk) : pick_score_kernel<Bf16Tag, false>(qpk);
+  else
+    kern = il ? pick_score_kernel<Fp16Tag, true>(qpk) : pick_score_kernel<Fp16Tag, false>(qpk);
+  if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: qpk %d unsupported", qpk);
+  dim3 grid(static_cast<unsigned>(s.max_tiles), static_cast<unsigned>(n_seq),
+            static_cast<unsigned>(n_layers));
+  if (n_seq > 65535 || n_layers > 65535)
+    return fail(KVC_EINVAL, "kvc_score_paged: too many sequences or layers for one launch");
+  kern<<<grid, kScoreThreads, 0, st>>>(sa);
+  return launch_status("kvc_score_paged");
+}
+
+extern "C" int kvc_head_stats(kvc_stream_t stream, int n_layers, int kv_heads, int head_dim,
+                              int rotary_dim, int qpk, int n_seq, int max_seq_len,
+                              const int32_t* seq_lens, const void* workspace,
+                              size_t workspace_bytes_given, float* mean, float* var) {
+  ScoreShape s;
+  if (!make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len))
+    return fail(KVC_EINVAL, "kvc_head_stats: unsupported shape");
+  if (!seq_lens || !workspace || !mean || !var)
+    return fail(KVC_EINVAL, "kvc_head_stats: null pointer");
+  if (workspace_bytes_given < workspace_bytes(s))
+    return fail(KVC_EINVAL, "kvc_head_stats: workspace too small");
+  const double* partials = reinterpret_cast<const double*>(
+      static_cast<const char*>(workspace) + weights_bytes_aligned(s));
+  const int n_heads = kv_heads * qpk;
+  const int64_t total = static_cast<int64_t>(n_layers) * n_seq * n_heads;
+  head_stats_kernel<<<static_cast<unsigned>(ceil_div(total, 64)), 64, 0, as_stream(stream)>>>(
+      n_layers, n_seq, n_heads, s.max_tiles > 0 ? s.max_tiles : 1, seq_lens, partials, mean, var);
+  return launch_status("kvc_head_stats");
+}
+
+extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int n_seq,
+                             int max_seq_len, const int32_t* seq_lens,
+                             const int64_t* token_offsets, const float* raw,
+                             int64_t raw_layer_stride, int64_t raw_token_stride,
+                             int64_t raw_head_stride, const float* mean, const float* var,
+                             int64_t stats_layer_stride, int64_t stats_seq_stride,
+                             int layer_aggregation, unsigned flags, float* agg) {
+  if (n_layers <= 0 || n_heads <= 0 || n_seq <= 0 || max_seq_len < 0)
+    return fail(KVC_EINVAL, "kvc_aggregate: sizes must be positive");
+  if (n_layers * n_heads > kAggMaxStats)
+    return fail(KVC_EINVAL, "kvc_aggregate: layers*heads %d exceeds %d", n_layers * n_heads,
+                kAggMaxStats);
+  if (layer_aggregation != KVC_LAYER_MEAN && layer_aggregation != KVC_LAYER_MAX)
+    return fail(KVC_EINVAL, "kvc_aggregate: unknown layer aggregation %d", layer_aggregation);
+  if (!seq_lens || !token_offsets || !raw || !mean || !var || !agg)
+    return fail(KVC_EINVAL, "kvc_aggregate: null pointer");
+  if (n_seq > 65535) return fail(KVC_EINVAL, "kvc_aggregate: too many sequences");
+  if (max_seq_len == 0) return 0;
+  AggArgs aa;
+  aa.n_layers = n_layers;
+  aa.n_heads = n_heads;
+  aa.n_seq = n_seq;
+  aa.layer_mode = layer_aggregation;
+  aa.flags = flags;
+  aa.seq_lens = seq_lens;
+  aa.token_offsets = token_offsets;
+  aa.raw = raw;
+  aa.raw_layer_stride = raw_layer_stride;
+  aa.raw_token_stride = raw_token_stride;
+  aa.raw_head_stride = raw_head_stride;
+  aa.mean = mean;
+  aa.var = var;
+  aa.stats_layer_stride = stats_layer_stride;
+  aa.stats_seq_stride = stats_seq_stride;
+  aa.agg = agg;
+  dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggThreads)), static_cast<unsigned>(n_seq));
+  aggregate_kernel<<<grid, kAggThreads, 0, as_stream(stream)>>>(aa);
+  return launch_status("kvc_aggregate");
+}

@@ -1,0 +1,17 @@
+"""Built-in TriAttention method (tri/__init__.py)."""
+
+from .config import TriAttentionConfig
+from .method import (
+    METHOD_NAME,
+    TriAttentionLayerCache,
+    TriAttentionMethod,
+    create_triattention_method,
+)
+
+__all__ = [
+    "METHOD_NAME",
+    "TriAttentionConfig",
+    "TriAttentionLayerCache",
+    "TriAttentionMethod",
+    "create_triattention_method",
+]

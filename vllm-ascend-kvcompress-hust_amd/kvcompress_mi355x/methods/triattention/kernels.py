@@ -1,0 +1,304 @@
+"""HIP entry points under the reference's kernel-wrapper names (tri/kernels.py).
+
+Each function keeps the reference signature and argument meaning.  Where the
+reference returns ``False`` for "not my device" so its caller can fall back to
+torch, these wrappers raise instead: the MI355X path has no host fallback.
+All work is enqueued on the current stream of the tensors' device.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ... import _native
+from . import _device as dev
+
+
+def prepare_mean_phase_coefficients(
+    omega: torch.Tensor,
+    offset_cos_mean: torch.Tensor,
+    offset_sin_mean: torch.Tensor,
+    round_start: int,
+    phase_cos: torch.Tensor,
+    phase_sin: torch.Tensor,
+) -> bool:
+    """Angle-addition phase table for every (layer, frequency) (tri/kernels.py:85-122)."""
+    for name, t in (
+        ("omega", omega),
+        ("offset_cos_mean", offset_cos_mean),
+        ("offset_sin_mean", offset_sin_mean),
+        ("phase_cos", phase_cos),
+        ("phase_sin", phase_sin),
+    ):
+        dev.require_hip(t, name)
+        dev.require_dtype(t, name, torch.float32)
+        dev.require_contiguous(t, name)
+    if not (omega.shape == offset_cos_mean.shape == offset_sin_mean.shape == phase_cos.shape == phase_sin.shape):
+        raise ValueError("phase coefficient tensors must have matching shapes")
+    _native.call(
+        "kvc_shift_mean_phases",
+        dev.stream_handle(omega.device),
+        int(omega.numel()),
+        int(round_start),
+        dev.ptr(omega),
+        dev.ptr(offset_cos_mean),
+        dev.ptr(offset_sin_mean),
+        dev.ptr(phase_cos),
+        dev.ptr(phase_sin),
+    )
+    return True
+
+
+def mean_phase_table(
+    round_starts: torch.Tensor, offsets: torch.Tensor, omega: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Directly evaluated phase means, as the torch scoring path forms them
+    (tri/scoring.py:77-80): [n_seq, layers, F] for int64 round_starts [n_seq]
+    and omega [layers, F]."""
+    for name, t in (("round_starts", round_starts), ("offsets", offsets), ("omega", omega)):
+        dev.require_hip(t, name)
+        dev.require_contiguous(t, name)
+    dev.require_dtype(round_starts, "round_starts", torch.int64)
+    dev.require_dtype(offsets, "offsets", torch.float32)
+    dev.require_dtype(omega, "omega", torch.float32)
+    if omega.ndim != 2 or round_starts.ndim != 1 or offsets.ndim != 1:
+        raise ValueError("expected round_starts [n], offsets [o], omega [layers, F]")
+    n_seq, (layers, freq) = int(round_starts.numel()), omega.shape
+    cos = torch.empty((n_seq, layers, freq), dtype=torch.float32, device=omega.device)
+    sin = torch.empty_like(cos)
+    _native.call(
+        "kvc_mean_phases",
+        dev.stream_handle(omega.device),
+        n_seq,
+        int(layers),
+        int(freq),
+        dev.ptr(round_starts),
+        dev.ptr(offsets),
+        int(offsets.numel()),
+        dev.ptr(omega),
+        dev.ptr(cos),
+        dev.ptr(sin),
+    )
+    return cos, sin
+
+
+def score_paged_keys_mean_precomputed(
+    k_cache: torch.Tensor,
+    source_block_ids: torch.Tensor,
+    q_real: torch.Tensor,
+    q_imag: torch.Tensor,
+    frequency_scale: torch.Tensor,
+    extra_coefficient: torch.Tensor,
+    phase_cos: torch.Tensor,
+    phase_sin: torch.Tensor,
+    num_tokens: int,
+    output: torch.Tensor,
+    block_size: int,
+    rope_style: str,
+    *,
+    q_pass_mean: torch.Tensor | None = None,
+    rotary_dim: int | None = None,
+) -> bool:
+    """Score one layer's paged keys with precomputed phases (tri/kernels.py:247-317).
+
+    ``output`` is [kv_heads, queries_per_kv, >= num_tokens] float32 with
+    contiguous query rows, as in the reference workspace layout."""
+    if block_size != 128:
+        raise ValueError("the HIP scorer addresses 128-token cache blocks")
+    dev.validate_cache(k_cache, "k_cache", block_size)
+    kv_heads, qpk, freq = q_real.shape
+    rotary = 2 * freq if rotary_dim is None else int(rotary_dim)
+    head_dim = int(k_cache.shape[-1])
+    if rotary != 2 * freq or not 0 < rotary <= head_dim:
+        raise ValueError("rotary_dim must match the calibrated frequency count")
+    pass_dim = head_dim - rotary
+    if pass_dim:
+        if q_pass_mean is None or tuple(q_pass_mean.shape) != (kv_heads, qpk, pass_dim):
+            raise ValueError("partial-RoPE scoring requires matching q_pass_mean")
+        if not q_pass_mean.is_contiguous():
+            raise ValueError("q_pass_mean must be contiguous")
+    elif q_pass_mean is not None:
+        raise ValueError("full-RoPE scoring must not pass q_pass_mean")
+    if int(k_cache.shape[2]) != kv_heads:
+        raise ValueError("calibration KV-head count does not match cache keys")
+    if k_cache.stride(0) % 8 or k_cache.data_ptr() % 16:
+        raise ValueError("the HIP scorer reads 16-byte words: page stride must be a multiple of 8 elements")
+    for name, t in (
+        ("q_real", q_real),
+        ("q_imag", q_imag),
+        ("frequency_scale", frequency_scale),
+        ("extra_coefficient", extra_coefficient),
+    ):
+        dev.require_hip(t, name)
+        if tuple(t.shape) != (kv_heads, qpk, freq):
+            raise ValueError(f"{name} must have shape {(kv_heads, qpk, freq)}")
+    for name, t in (("phase_cos", phase_cos), ("phase_sin", phase_sin)):
+        dev.require_hip(t, name)
+        if t.numel() != freq:
+            raise ValueError(f"{name} must hold {freq} values")
+    dev.require_hip(output, "output")
+    dev.require_dtype(output, "output", torch.float32)
+    if output.ndim != 3 or tuple(output.shape[:2]) != (kv_heads, qpk) or output.shape[2] < num_tokens:
+        raise ValueError("output must be [kv_heads, queries_per_kv, >= num_tokens]")
+    if output.stride(2) != 1 or output.stride(0) != qpk * output.stride(1):
+        raise ValueError("output query rows must be contiguous and evenly strided")
+    num_tokens = int(num_tokens)
+    blocks = source_block_ids.to(dtype=torch.int64).contiguous()
+    dev.require_hip(blocks, "source_block_ids")
+    if blocks.numel() * block_size < num_tokens:
+        raise ValueError("source block table does not cover num_tokens")
+    device = k_cache.device
+
+    def f32(t: torch.Tensor) -> torch.Tensor:
+        return t.to(dtype=torch.float32).contiguous()
+
+    layer_ptrs = dev.pointer_table([k_cache], device)
+    seq_lens = torch.tensor([num_tokens], dtype=torch.int32, device=device)
+    token_offsets = torch.tensor([0, num_tokens], dtype=torch.int64, device=device)
+    block_offsets = torch.tensor([0, blocks.numel()], dtype=torch.int64, device=device)
+    q_pass = f32(q_pass_mean) if q_pass_mean is not None else None
+    qr, qi, sc, ex = f32(q_real), f32(q_imag), f32(frequency_scale), f32(extra_coefficient)
+    pc, ps = f32(phase_cos.reshape(-1)), f32(phase_sin.reshape(-1))
+    ws_bytes = _native.load().kvc_score_workspace_bytes(1, kv_heads, head_dim, rotary, qpk, 1, max(num_tokens, 1))
+    if ws_bytes == 0:
+        raise ValueError("unsupported scoring shape for the MI355X kernel")
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    _native.call(
+        "kvc_score_paged",
+        dev.stream_handle(device),
+        dev.cache_dtype_code(k_cache.dtype),
+        1,
+        dev.ptr(layer_ptrs),
+        int(k_cache.shape[0]),
+        int(k_cache.stride(0)),
+        kv_heads,
+        head_dim,
+        rotary,
+        qpk,
+        dev.rope_style_code(rope_style),
+        1,
+        num_tokens,
+        dev.ptr(seq_lens),
+        dev.ptr(token_offsets),
+        dev.ptr(block_offsets),
+        dev.ptr(blocks),
+        dev.ptr(qr),
+        dev.ptr(qi),
+        dev.ptr(sc),
+        dev.ptr(ex),
+        dev.ptr(q_pass),
+        dev.ptr(pc),
+        dev.ptr(ps),
+        0,
+        dev.ptr(output),
+        0,
+        1,
+        int(output.stride(1)),
+        dev.ptr(workspace),
+        ws_bytes,
+    )
+    return True
+
+
+def score_paged_keys_mean(
+    k_cache: torch.Tensor,
+    source_block_ids: torch.Tensor,
+    q_real: torch.Tensor,
+    q_imag: torch.Tensor,
+    frequency_scale: torch.Tensor,
+    extra_coefficient: torch.Tensor,
+    omega: torch.Tensor,
+    offset_cos_mean: torch.Tensor,
+    offset_sin_mean: torch.Tensor,
+    round_start: int,
+    num_tokens: int,
+    output: torch.Tensor,
+    block_size: int,
+    rope_style: str,
+    *,
+    q_pass_mean: torch.Tensor | None = None,
+    rotary_dim: int | None = None,
+) -> bool:
+    """Compatibility form that prepares one layer's phases (tri/kernels.py:320-362)."""
+    phase_cos = torch.empty_like(omega, dtype=torch.float32)
+    phase_sin = torch.empty_like(phase_cos)
+    prepare_mean_phase_coefficients(
+        omega.float().contiguous(),
+        offset_cos_mean.float().contiguous(),
+        offset_sin_mean.float().contiguous(),
+        round_start,
+        phase_cos,
+        phase_sin,
+    )
+    return score_paged_keys_mean_precomputed(
+        k_cache,
+        source_block_ids,
+        q_real,
+        q_imag,
+        frequency_scale,
+        extra_coefficient,
+        phase_cos,
+        phase_sin,
+        num_tokens,
+        output,
+        block_size,
+        rope_style,
+        q_pass_mean=q_pass_mean,
+        rotary_dim=rotary_dim,
+    )
+
+
+def aggregate_normalized_scores(
+    scores: torch.Tensor,
+    mean: torch.Tensor,
+    variance: torch.Tensor,
+    aggregate: torch.Tensor,
+    num_tokens: int,
+    *,
+    layer_aggregation: str,
+    first_layer: bool,
+) -> bool:
+    """Normalise, max over query heads, accumulate one layer (tri/kernels.py:407-437).
+
+    Uses the reference device kernel's rsqrt form; ``scores`` is
+    [kv_heads, queries_per_kv, >= num_tokens] with evenly strided query rows."""
+    for name, t in (("scores", scores), ("mean", mean), ("variance", variance), ("aggregate", aggregate)):
+        dev.require_hip(t, name)
+        dev.require_dtype(t, name, torch.float32)
+    if layer_aggregation not in ("mean", "max"):
+        raise ValueError(f"unsupported layer aggregation {layer_aggregation!r}")
+    heads = int(mean.numel())
+    if scores.stride(-1) != 1:
+        raise ValueError("score rows must be contiguous")
+    flat_scores = scores.reshape(heads, scores.shape[-1]) if scores.ndim == 3 else scores
+    if flat_scores.shape[0] != heads or variance.numel() != heads:
+        raise ValueError("mean/variance must hold one value per query head")
+    num_tokens = int(num_tokens)
+    device = scores.device
+    m = mean.reshape(-1).contiguous()
+    v = variance.reshape(-1).contiguous()
+    seq_lens = torch.tensor([num_tokens], dtype=torch.int32, device=device)
+    token_offsets = torch.tensor([0, num_tokens], dtype=torch.int64, device=device)
+    flags = _native.AGG_RSQRT | (0 if first_layer else _native.AGG_ACCUMULATE)
+    _native.call(
+        "kvc_aggregate",
+        dev.stream_handle(device),
+        1,
+        heads,
+        1,
+        num_tokens,
+        dev.ptr(seq_lens),
+        dev.ptr(token_offsets),
+        dev.ptr(flat_scores),
+        0,
+        1,
+        int(flat_scores.stride(0)),
+        dev.ptr(m),
+        dev.ptr(v),
+        0,
+        0,
+        _native.LAYER_MEAN if layer_aggregation == "mean" else _native.LAYER_MAX,
+        flags,
+        dev.ptr(aggregate),
+    )
+    return True

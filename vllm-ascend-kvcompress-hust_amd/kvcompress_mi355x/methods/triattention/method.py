@@ -1,0 +1,212 @@
+"""TriAttentionMethod: the method API v1 implementation on MI355X.
+
+Keeps the reference's lifecycle and contracts (tri/method.py:57-515):
+``runtime_spec`` advertises private destinations, the compression threshold
+(budget + recompute window) and the physical budget; ``bind_model_runner``
+validates the bound caches against the calibration, precomputes the scoring
+tables for every ``score_layer_stride``-th layer and allocates address-stable
+device buffers; ``compress`` scores the sampled layers, selects the keep set
+and materialises it into the destination blocks of every bound layer,
+returning ``CompressionResult(budget, ((layer, budget), ...))``.
+
+``compress_batch`` runs many requests in one batched step (one launch per
+kernel for the whole batch); ``compress`` is the one-request case of it.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping, Sequence
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from ...config import KERNEL_BLOCK_SIZE, JsonScalar
+from ..base import (
+    CompressionRequest,
+    CompressionResult,
+    KVCompressionMethod,
+    LayerCache,
+    MethodRuntimeSpec,
+    ModelShape,
+)
+from . import _device as dev
+from .config import TriAttentionConfig
+from .pipeline import Batch, CompressionPipeline, ScoringTables
+from .scoring import build_geometric_offsets
+from .stats import CalibrationStats, DeviceLayerCalibrationStats
+
+METHOD_NAME = "triattention"
+MTP_LAYER_NAME = "mtp.layers.0.self_attn.attn"
+
+
+def queries_per_kv_head(model_shape: ModelShape) -> int:
+    if model_shape.num_attention_heads % model_shape.num_kv_heads:
+        raise RuntimeError("TriAttention requires query heads divisible by KV heads")
+    return model_shape.num_attention_heads // model_shape.num_kv_heads
+
+
+def is_mtp_cache_layer(layer_name: str) -> bool:
+    return ".mtp.layers." in f".{layer_name}."
+
+
+@dataclass(frozen=True)
+class TriAttentionLayerCache:
+    name: str
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    stats: DeviceLayerCalibrationStats
+
+
+class TriAttentionMethod(KVCompressionMethod):
+    """TriAttention KV selection with MI355X HIP kernels behind method API v1."""
+
+    def __init__(self, options: Mapping[str, JsonScalar], vllm_config: Any, model_shape: ModelShape) -> None:
+        self.config = TriAttentionConfig.from_method_config(options)
+        if self.config.score_aggregation != "mean":
+            raise ValueError(
+                "score_aggregation 'max' is not implemented by the MI355X scorer; use 'mean'"
+            )
+        self.vllm_config = vllm_config
+        self.model_shape = model_shape
+        self.calibration = CalibrationStats.load(self.config.stats_path)
+        self.layer_caches: tuple[TriAttentionLayerCache, ...] = ()
+        self.materialization_caches: tuple[LayerCache, ...] = ()
+        self.cache_block_size = KERNEL_BLOCK_SIZE
+        self.offsets: torch.Tensor | None = None
+        self.pipeline: CompressionPipeline | None = None
+
+    @property
+    def name(self) -> str:
+        return METHOD_NAME
+
+    @property
+    def runtime_spec(self) -> MethodRuntimeSpec:
+        return MethodRuntimeSpec(
+            requires_private_destination=True,
+            compression_threshold_tokens=self.config.compression_threshold_tokens,
+            required_recompute_tokens=self.config.recompute_window,
+            max_physical_num_tokens=self.config.kv_budget,
+            min_output_tokens_for_compression=self.config.min_output_tokens_for_compression,
+        )
+
+    def compatibility_reasons(self, worker: Any) -> tuple[str, ...]:
+        del worker
+        return self.calibration.validate(self.model_shape)
+
+    # ---------------------------------------------------------------- bind --
+    def bind_model_runner(self, runner: Any, layer_caches: tuple[LayerCache, ...]) -> None:
+        tp_size = int(getattr(getattr(self.vllm_config, "parallel_config", None), "tensor_parallel_size", 1))
+        if tp_size != 1:
+            raise RuntimeError("the MI355X TriAttention path runs on one GPU (tensor_parallel_size 1)")
+        device = torch.device(runner.device)
+        if device.type != "cuda":
+            raise RuntimeError("TriAttention on MI355X requires a HIP device")
+        max_len = int(self.vllm_config.model_config.max_model_len)
+        device_stats = self.calibration.to_device(self.model_shape, device)
+        self.offsets = build_geometric_offsets(max_len, device)
+
+        mtp = tuple(layer for layer in layer_caches if is_mtp_cache_layer(layer.name))
+        target = tuple(layer for layer in layer_caches if not is_mtp_cache_layer(layer.name))
+        speculative = getattr(self.vllm_config, "speculative_config", None)
+        if mtp and (
+            len(mtp) != 1
+            or mtp[0].name != MTP_LAYER_NAME
+            or getattr(speculative, "method", None) != "mtp"
+            or getattr(speculative, "num_speculative_tokens", None) != 2
+        ):
+            raise RuntimeError("uncalibrated MTP cache requires Qwen3.5 MTP2")
+        if len(target) != len(self.model_shape.full_attention_layer_indices):
+            raise RuntimeError("allocated full-attention layer count does not match calibration")
+        bound: list[TriAttentionLayerCache] = []
+        seen: set[int] = set()
+        for layer in target:
+            if layer.layer_index not in device_stats:
+                raise RuntimeError(
+                    f"attention layer {layer.name!r} resolves to invalid model layer index {layer.layer_index}"
+                )
+            if layer.layer_index in seen:
+                raise RuntimeError(f"multiple cache layers resolve to model layer index {layer.layer_index}")
+            seen.add(layer.layer_index)
+            bound.append(TriAttentionLayerCache(layer.name, layer.k_cache, layer.v_cache, device_stats[layer.layer_index]))
+        expected = set(self.model_shape.full_attention_layer_indices)
+        if seen != expected:
+            raise RuntimeError(
+                "allocated target full-attention layers do not match calibration: "
+                f"allocated={sorted(seen)} expected={sorted(expected)}"
+            )
+        self.layer_caches = tuple(bound)
+        self.materialization_caches = tuple(layer_caches)
+        cache = self.layer_caches[0].k_cache
+        self.cache_block_size = int(cache.shape[1])
+        if self.cache_block_size != KERNEL_BLOCK_SIZE:
+            raise RuntimeError("TriAttention requires 128-token kernel cache blocks")
+        if int(cache.shape[2]) != self.model_shape.num_kv_heads:
+            raise RuntimeError(
+                "local KV-cache head count does not match the model shape: "
+                f"expected {self.model_shape.num_kv_heads}, got {cache.shape[2]}"
+            )
+        queries_per_kv_head(self.model_shape)
+        scoring = self.layer_caches[:: self.config.score_layer_stride]
+        tables = ScoringTables.from_layer_stats([layer.stats for layer in scoring], self.offsets)
+        self.pipeline = CompressionPipeline(
+            scoring_k_caches=[layer.k_cache for layer in scoring],
+            k_caches=[layer.k_cache for layer in self.materialization_caches],
+            v_caches=[layer.v_cache for layer in self.materialization_caches],
+            tables=tables,
+            budget=self.config.kv_budget,
+            protected_prefix=self.config.protected_prefix_window,
+            protected_recent=self.config.protected_recent_window,
+            segments=self.config.position_segments,
+            policy=self.config.position_policy,
+            layer_aggregation=self.config.layer_aggregation,
+            max_seqs=1,
+            max_seq_len=max_len,
+        )
+
+    # ------------------------------------------------------------ compress --
+    def _result(self) -> CompressionResult:
+        return CompressionResult(
+            physical_num_tokens=self.config.kv_budget,
+            per_layer_physical_num_tokens=tuple(
+                (layer.name, self.config.kv_budget) for layer in self.materialization_caches
+            ),
+        )
+
+    def compress(self, request: CompressionRequest) -> CompressionResult:
+        return self.compress_batch((request,))[0]
+
+    def compress_batch(self, requests: Sequence[CompressionRequest]) -> list[CompressionResult]:
+        """Compress many scheduler-authorised requests in one batched step."""
+        if self.pipeline is None or self.offsets is None or not self.layer_caches:
+            raise RuntimeError("TriAttention method is not bound to KV cache")
+        if not requests:
+            return []
+        for request in requests:
+            dev.require_hip(request.source_block_ids_device, "source_block_ids_device")
+            dev.require_hip(request.destination_block_ids_device, "destination_block_ids_device")
+        batch = Batch.build(
+            self.pipeline.device,
+            [int(r.physical_num_tokens) for r in requests],
+            [int(r.semantic_num_tokens) for r in requests],
+            [r.source_block_ids_device for r in requests],
+            [r.destination_block_ids_device for r in requests],
+            block_size=self.cache_block_size,
+            budget=self.config.kv_budget,
+        )
+        self.pipeline.select_step(batch)
+        self.pipeline.compact(batch)
+        return [self._result() for _ in requests]
+
+    def select_keep_indices(self, source_block_ids: torch.Tensor, physical_num_tokens: int, round_start: int) -> torch.Tensor:
+        """Keep indices of one request without materialising (tri/method.py:297-475)."""
+        if self.pipeline is None:
+            raise RuntimeError("TriAttention method is not bound to KV cache")
+        batch = Batch.build(self.pipeline.device, [int(physical_num_tokens)], [int(round_start)], [source_block_ids])
+        return self.pipeline.select_step(batch)[0].clone()
+
+
+def create_triattention_method(
+    options: Mapping[str, JsonScalar], vllm_config: Any, model_shape: ModelShape
+) -> KVCompressionMethod:
+    return TriAttentionMethod(options, vllm_config, model_shape)

@@ -1,0 +1,416 @@
+"""Batched TriAttention compression step on one GPU.
+
+One call of :meth:`CompressionPipeline.step` runs, for every sequence of a
+batch at once, the work the reference does per request in
+TriAttentionMethod._select_keep_indices and compress (tri/method.py:256-475):
+
+  1. phase table      kvc_mean_phases      [n_seq, S, F]
+  2. score            kvc_score_paged      raw [S, sum N, H_q] + partial sums
+  3. head statistics  kvc_head_stats       mean/var [S, n_seq, H_q]
+  4. aggregate        kvc_aggregate        agg [sum N] (head max, layer mean, sanitise)
+  5. select           kvc_select_keep      keep [n_seq, budget] ascending
+  6. compact          kvc_compact          kept K/V rows of every layer
+  7. block tables     kvc_rewrite_block_tables
+
+Everything is enqueued on the current stream; nothing synchronises.  Device
+buffers are sized once for a capacity (sequences, tokens, longest sequence)
+and reused, as the reference keeps address-stable workspaces
+(tri/method.py:205-254).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from ... import _native
+from . import _device as dev
+from .cache import compact_layers, rewrite_block_tables
+from .selection import POLICY_CODES, validate_selection
+
+
+@dataclass(frozen=True)
+class ScoringTables:
+    """Calibration of the scoring layers, stacked for the kernel.
+
+    q_real, q_imag, freq_scale (sqrt of freq_scale_sq), extra
+    (q_abs_mean - sqrt(q_real^2 + q_imag^2 + 1e-8)): [S, kv_heads, qpk, F];
+    q_pass: [S, kv_heads, qpk, P] or None; omega: [S, F]; offsets: [n_offsets].
+    """
+
+    q_real: torch.Tensor
+    q_imag: torch.Tensor
+    freq_scale: torch.Tensor
+    extra: torch.Tensor
+    q_pass: torch.Tensor | None
+    omega: torch.Tensor
+    offsets: torch.Tensor
+    rotary_dim: int
+    rope_style: str = "half"
+
+    @property
+    def n_layers(self) -> int:
+        return int(self.q_real.shape[0])
+
+    @property
+    def kv_heads(self) -> int:
+        return int(self.q_real.shape[1])
+
+    @property
+    def qpk(self) -> int:
+        return int(self.q_real.shape[2])
+
+    @property
+    def freq(self) -> int:
+        return int(self.q_real.shape[3])
+
+    @classmethod
+    def from_layer_stats(cls, stats: list, offsets: torch.Tensor) -> ScoringTables:
+        """Stack DeviceLayerCalibrationStats of the scoring layers, with the
+        bind-time precompute of tri/method.py:161-165."""
+        q_real = torch.stack([s.q_mean_real for s in stats]).float().contiguous()
+        q_imag = torch.stack([s.q_mean_imag for s in stats]).float().contiguous()
+        scale = torch.sqrt(torch.stack([s.freq_scale_sq for s in stats]).float()).contiguous()
+        q_abs = torch.stack([s.q_abs_mean for s in stats]).float()
+        extra = (q_abs - torch.sqrt(q_real.square() + q_imag.square() + 1e-8)).contiguous()
+        passes = [s.q_pass_mean for s in stats]
+        q_pass = None if passes[0] is None else torch.stack(passes).float().contiguous()
+        omega = torch.stack([s.omega for s in stats]).float().contiguous()
+        rotary = stats[0].rotary_dim if stats[0].rotary_dim is not None else 2 * int(q_real.shape[-1])
+        return cls(q_real, q_imag, scale, extra, q_pass, omega, offsets.float().contiguous(), int(rotary), stats[0].rope_style)
+
+
+@dataclass
+class Batch:
+    """Device descriptors of one batch of sequences."""
+
+    n_seq: int
+    seq_lens_host: list[int]
+    round_starts_host: list[int]
+    src_lengths_host: list[int]
+    seq_lens: torch.Tensor
+    token_offsets: torch.Tensor
+    round_starts: torch.Tensor
+    src_offsets: torch.Tensor
+    src_ids: torch.Tensor
+    dst_offsets: torch.Tensor | None
+    dst_ids: torch.Tensor | None
+    rewrite_buffers: dict = field(default_factory=dict)
+
+    @property
+    def total_tokens(self) -> int:
+        return sum(self.seq_lens_host)
+
+    @property
+    def inplace(self) -> bool:
+        return self.dst_ids is None
+
+    @classmethod
+    def build(
+        cls,
+        device: torch.device,
+        seq_lens: list[int],
+        round_starts: list[int],
+        source_tables: list,
+        destination_tables: list | None = None,
+        *,
+        block_size: int = 128,
+        budget: int | None = None,
+    ) -> Batch:
+        n = len(seq_lens)
+        if n == 0 or len(round_starts) != n or len(source_tables) != n:
+            raise ValueError("a batch needs matching lengths, round starts and source tables")
+        src_off, src_ids, src_lens = dev.ragged(list(source_tables), device)
+        for length, blocks in zip(seq_lens, src_lens):
+            if length < 0 or blocks * block_size < length:
+                raise ValueError("source block table does not cover the sequence")
+        dst_off = dst_ids = None
+        if destination_tables is not None:
+            if len(destination_tables) != n:
+                raise ValueError("one destination table per sequence")
+            dst_off, dst_ids, dst_lens = dev.ragged(list(destination_tables), device)
+            if budget is not None:
+                need = (budget + block_size - 1) // block_size
+                if any(d < need for d in dst_lens):
+                    raise ValueError("destination table too short for the budget")
+        offsets = [0]
+        for length in seq_lens:
+            offsets.append(offsets[-1] + int(length))
+        return cls(
+            n_seq=n,
+            seq_lens_host=[int(x) for x in seq_lens],
+            round_starts_host=[int(x) for x in round_starts],
+            src_lengths_host=src_lens,
+            seq_lens=torch.tensor(seq_lens, dtype=torch.int32, device=device),
+            token_offsets=torch.tensor(offsets, dtype=torch.int64, device=device),
+            round_starts=torch.tensor(round_starts, dtype=torch.int64, device=device),
+            src_offsets=src_off,
+            src_ids=src_ids,
+            dst_offsets=dst_off,
+            dst_ids=dst_ids,
+        )
+
+
+class CompressionPipeline:
+    """Device state and launches of the batched compression step."""
+
+    def __init__(
+        self,
+        *,
+        scoring_k_caches: list[torch.Tensor],
+        k_caches: list[torch.Tensor],
+        v_caches: list[torch.Tensor],
+        tables: ScoringTables,
+        budget: int,
+        protected_prefix: int,
+        protected_recent: int,
+        segments: int,
+        policy: str,
+        layer_aggregation: str,
+        max_seqs: int,
+        max_seq_len: int,
+        max_tokens: int | None = None,
+    ) -> None:
+        if not scoring_k_caches or len(scoring_k_caches) != tables.n_layers:
+            raise ValueError("one scoring K cache per scoring layer is required")
+        if not k_caches or len(k_caches) != len(v_caches):
+            raise ValueError("matching K and V cache lists are required")
+        reference = k_caches[0]
+        for i, cache in enumerate([*scoring_k_caches, *k_caches, *v_caches]):
+            dev.validate_cache(cache, f"cache[{i}]")
+            if cache.shape != reference.shape or cache.stride() != reference.stride() or cache.dtype != reference.dtype:
+                raise ValueError("every cache layer must share shape, strides and dtype")
+            if cache.data_ptr() % 16 or cache.stride(0) % 8:
+                raise ValueError("cache base addresses and page strides must be 16-byte aligned")
+        if layer_aggregation not in ("mean", "max"):
+            raise ValueError(f"unsupported layer aggregation {layer_aggregation!r}")
+        if policy not in POLICY_CODES:
+            raise ValueError(f"unsupported position policy: {policy}")
+        self.device = reference.device
+        self.dtype = reference.dtype
+        self.num_pages = int(reference.shape[0])
+        self.page_stride = int(reference.stride(0))
+        self.kv_heads = int(reference.shape[2])
+        self.head_dim = int(reference.shape[3])
+        self.row_elems = self.kv_heads * self.head_dim
+        if tables.kv_heads != self.kv_heads:
+            raise ValueError("calibration KV-head count does not match cache keys")
+        if 2 * tables.freq != tables.rotary_dim or tables.rotary_dim > self.head_dim:
+            raise ValueError("calibration frequency count does not match cache keys")
+        pass_dim = self.head_dim - tables.rotary_dim
+        if pass_dim and (tables.q_pass is None or tables.q_pass.shape[-1] != pass_dim):
+            raise ValueError("partial-RoPE scoring requires q_pass_mean")
+        self.tables = tables
+        self.budget = int(budget)
+        self.protected_prefix = int(protected_prefix)
+        self.protected_recent = int(protected_recent)
+        self.segments = int(segments)
+        self.policy = policy
+        self.layer_aggregation = layer_aggregation
+        self.n_heads = tables.kv_heads * tables.qpk
+        self.scoring_ptrs = dev.pointer_table(scoring_k_caches, self.device)
+        self.k_ptrs = dev.pointer_table(k_caches, self.device)
+        self.v_ptrs = dev.pointer_table(v_caches, self.device)
+        self._caches = (scoring_k_caches, k_caches, v_caches)  # keep the bound storage alive
+        self._allocate(max_seqs, max_seq_len, max_tokens or max_seqs * max_seq_len)
+
+    # ------------------------------------------------------------ buffers --
+    def _allocate(self, max_seqs: int, max_seq_len: int, max_tokens: int) -> None:
+        s = self.tables.n_layers
+        self.max_seqs, self.max_seq_len, self.max_tokens = int(max_seqs), int(max_seq_len), int(max_tokens)
+        dev_ = self.device
+        self.phase_cos = torch.empty((self.max_seqs, s, self.tables.freq), dtype=torch.float32, device=dev_)
+        self.phase_sin = torch.empty_like(self.phase_cos)
+        self.raw = torch.empty((s, self.max_tokens, self.n_heads), dtype=torch.float32, device=dev_)
+        self.mean = torch.empty((s, self.max_seqs, self.n_heads), dtype=torch.float32, device=dev_)
+        self.var = torch.empty_like(self.mean)
+        self.agg = torch.empty(self.max_tokens, dtype=torch.float32, device=dev_)
+        self.keep = torch.empty((self.max_seqs, self.budget), dtype=torch.int64, device=dev_)
+        ws = _native.load().kvc_score_workspace_bytes(
+            s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len
+        )
+        if ws == 0:
+            raise ValueError("unsupported scoring shape for the MI355X kernel")
+        self.workspace_bytes = int(ws)
+        self.workspace = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=dev_)
+
+    def ensure_capacity(self, batch: Batch) -> None:
+        if (
+            batch.n_seq > self.max_seqs
+            or max(batch.seq_lens_host) > self.max_seq_len
+            or batch.total_tokens > self.max_tokens
+        ):
+            self._allocate(
+                max(batch.n_seq, self.max_seqs),
+                max(max(batch.seq_lens_host), self.max_seq_len),
+                max(batch.total_tokens, self.max_tokens),
+            )
+
+    def validate(self, batch: Batch) -> None:
+        for n in batch.seq_lens_host:
+            validate_selection(
+                n,
+                budget=self.budget,
+                protected_prefix=self.protected_prefix,
+                protected_recent=self.protected_recent,
+                segments=self.segments,
+                policy=self.policy,
+            )
+
+    # -------------------------------------------------------------- steps --
+    def score(self, batch: Batch) -> None:
+        """Phase table, raw scores and head statistics."""
+        t = self.tables
+        stream = dev.stream_handle(self.device)
+        max_len = max(batch.seq_lens_host)
+        _native.call(
+            "kvc_mean_phases",
+            stream,
+            batch.n_seq,
+            t.n_layers,
+            t.freq,
+            dev.ptr(batch.round_starts),
+            dev.ptr(t.offsets),
+            int(t.offsets.numel()),
+            dev.ptr(t.omega),
+            dev.ptr(self.phase_cos),
+            dev.ptr(self.phase_sin),
+        )
+        _native.call(
+            "kvc_score_paged",
+            stream,
+            dev.cache_dtype_code(self.dtype),
+            t.n_layers,
+            dev.ptr(self.scoring_ptrs),
+            self.num_pages,
+            self.page_stride,
+            self.kv_heads,
+            self.head_dim,
+            t.rotary_dim,
+            t.qpk,
+            dev.rope_style_code(t.rope_style),
+            batch.n_seq,
+            max_len,
+            dev.ptr(batch.seq_lens),
+            dev.ptr(batch.token_offsets),
+            dev.ptr(batch.src_offsets),
+            dev.ptr(batch.src_ids),
+            dev.ptr(t.q_real),
+            dev.ptr(t.q_imag),
+            dev.ptr(t.freq_scale),
+            dev.ptr(t.extra),
+            dev.ptr(t.q_pass),
+            dev.ptr(self.phase_cos),
+            dev.ptr(self.phase_sin),
+            t.n_layers * t.freq,
+            dev.ptr(self.raw),
+            int(self.raw.stride(0)),
+            int(self.raw.stride(1)),
+            1,
+            dev.ptr(self.workspace),
+            self.workspace_bytes,
+        )
+        _native.call(
+            "kvc_head_stats",
+            stream,
+            t.n_layers,
+            self.kv_heads,
+            self.head_dim,
+            t.rotary_dim,
+            t.qpk,
+            batch.n_seq,
+            max_len,
+            dev.ptr(batch.seq_lens),
+            dev.ptr(self.workspace),
+            self.workspace_bytes,
+            dev.ptr(self.mean),
+            dev.ptr(self.var),
+        )
+
+    def aggregate(self, batch: Batch) -> None:
+        t = self.tables
+        _native.call(
+            "kvc_aggregate",
+            dev.stream_handle(self.device),
+            t.n_layers,
+            self.n_heads,
+            batch.n_seq,
+            max(batch.seq_lens_host),
+            dev.ptr(batch.seq_lens),
+            dev.ptr(batch.token_offsets),
+            dev.ptr(self.raw),
+            int(self.raw.stride(0)),
+            int(self.raw.stride(1)),
+            1,
+            dev.ptr(self.mean),
+            dev.ptr(self.var),
+            int(self.mean.stride(0)),
+            int(self.mean.stride(1)),
+            _native.LAYER_MEAN if self.layer_aggregation == "mean" else _native.LAYER_MAX,
+            _native.AGG_FINALIZE,
+            dev.ptr(self.agg),
+        )
+
+    def select(self, batch: Batch) -> torch.Tensor:
+        _native.call(
+            "kvc_select_keep",
+            dev.stream_handle(self.device),
+            batch.n_seq,
+            max(batch.seq_lens_host),
+            dev.ptr(batch.seq_lens),
+            dev.ptr(batch.token_offsets),
+            dev.ptr(self.agg),
+            self.budget,
+            self.protected_prefix,
+            self.protected_recent,
+            self.segments,
+            POLICY_CODES[self.policy],
+            dev.ptr(self.keep),
+            int(self.keep.stride(0)),
+        )
+        return self.keep[: batch.n_seq]
+
+    def compact(self, batch: Batch) -> None:
+        compact_layers(
+            self.k_ptrs,
+            self.v_ptrs,
+            num_pages=self.num_pages,
+            page_stride=self.page_stride,
+            row_elems=self.row_elems,
+            seq_lens=batch.seq_lens,
+            src_block_offsets=batch.src_offsets,
+            src_block_ids=batch.src_ids,
+            dst_block_offsets=batch.dst_offsets,
+            dst_block_ids=batch.dst_ids,
+            keep=self.keep,
+            budget=self.budget,
+        )
+
+    def rewrite(self, batch: Batch) -> tuple[torch.Tensor, list[torch.Tensor]]:
+        return rewrite_block_tables(
+            budget=self.budget,
+            src_block_offsets=batch.src_offsets,
+            src_block_ids=batch.src_ids,
+            src_lengths=batch.src_lengths_host,
+            dst_block_offsets=batch.dst_offsets,
+            dst_block_ids=batch.dst_ids,
+            buffers=batch.rewrite_buffers,
+        )
+
+    def select_step(self, batch: Batch) -> torch.Tensor:
+        """Score, aggregate and select: the keep indices of every sequence."""
+        self.validate(batch)
+        self.ensure_capacity(batch)
+        self.score(batch)
+        self.aggregate(batch)
+        return self.select(batch)
+
+    def step(self, batch: Batch, *, rewrite: bool = True) -> tuple[torch.Tensor, torch.Tensor | None, list[torch.Tensor] | None]:
+        """The whole compression step for a batch."""
+        keep = self.select_step(batch)
+        self.compact(batch)
+        if not rewrite:
+            return keep, None, None
+        tables, freed = self.rewrite(batch)
+        return keep, tables, freed
