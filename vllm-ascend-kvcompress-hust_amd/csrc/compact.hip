@@ -2,24 +2,27 @@
 //
 // Row i (< budget) of sequence b's destination receives source row keep[b][i].
 // A row is the kv_heads*head_dim elements of one token, contiguous inside its
-// page (reference cache layout [pages][128][kv_heads][head_dim]).  A
-// workgroup moves a tile of rows x a slice of columns in `Chunk`-sized words;
-// each thread issues all of its loads for the tile before its stores so a
-// lane keeps several requests in flight.
+// page (reference cache layout [pages][128][kv_heads][head_dim]).  Rows are
+// moved in `Chunk`-sized words by a thread layout of (row lane, column):
+// `slice_w` consecutive threads cover a slice of one row, so every wave
+// instruction reads and writes whole 128-byte lines.
 //
-// Private mode (destination pages disjoint from the source pages): every tile
-// is independent; the grid spans (row tile x column slice, sequence,
-// layer x {K,V}).
+// Private mode (destination pages disjoint from the source pages): a
+// workgroup owns a tile of rows x one column slice of one sequence.  It
+// resolves the rows' source and destination offsets once (keep index ->
+// source page -> byte offset) and then walks every layer, loading the K and V
+// words of the tile together before storing them, so the index chase is paid
+// once per tile instead of once per layer.
 //
 // In-place mode (destinations are the sequence's own front pages): keep is
 // strictly increasing, so keep[j] >= j and the source row of destination j can
-// only be overwritten by a destination i >= j.  A workgroup therefore owns one
-// column slice of one (layer, K/V, sequence) and walks the rows in ascending
-// tiles: all loads of a tile complete before a workgroup barrier, then the
+// only be overwritten by a destination i >= j.  A workgroup owns one column
+// slice of one (layer, sequence) and walks the rows in ascending tiles: every
+// load of a tile (K and V) completes before a workgroup barrier, then the
 // tile's stores go out.  A row read by tile T lies at index >= the first row
 // of tile T, so it is overwritten, if at all, by tile T itself (after the
-// barrier) or a later tile.  Column slices are disjoint bytes, so slices run
-// in parallel.  Rows whose source and destination coincide are skipped.
+// barrier) or by a later tile.  Column slices are disjoint bytes, so slices
+// run in parallel.  Rows whose source and destination coincide are skipped.
 
 #include "kvc_common.h"
 
@@ -27,19 +30,22 @@ namespace kvc {
 namespace {
 
 constexpr int kCopyThreads = 256;
-constexpr int kCopyUnroll = 8;  // rows in flight per thread
+constexpr int kCopyUnroll = 8;  // rows per thread per tile
+
+// Native vector words (the HIP_vector_type structs would be kept in scratch).
+typedef uint32_t w128 __attribute__((ext_vector_type(4)));
+typedef uint32_t w64 __attribute__((ext_vector_type(2)));
 
 struct CompactArgs {
   const uint64_t* k_ptrs;
   const uint64_t* v_ptrs;
+  int n_layers;
   int64_t num_pages;
   int64_t page_stride_bytes;
   int64_t row_bytes;
   int64_t row_chunks;    // row_bytes / sizeof(Chunk)
   int slice_shift;       // log2(chunks per column slice)
   int n_slices;
-  int n_row_tiles;       // private mode: row tiles per sequence
-  int inplace;
   int budget;
   const int32_t* seq_lens;
   const int64_t* src_off;
@@ -58,67 +64,123 @@ __device__ __forceinline__ int64_t page_of(const int64_t* table, int64_t n_entri
   return (p >= 0 && p < num_pages) ? p : -1;
 }
 
+// Byte offsets (inside one layer's buffer) of the source and destination word
+// of row `i`, or -1 when the row is out of range, unmapped or already in place.
+struct RowMove {
+  int64_t src, dst;
+};
+
+__device__ __forceinline__ RowMove resolve_row(const CompactArgs& a, const int64_t* sbt, int64_t n_src,
+                                               const int64_t* dbt, int64_t n_dst, const int64_t* kp,
+                                               int64_t n_tokens, int64_t i, int64_t word_off,
+                                               bool col_ok) {
+  RowMove m{-1, -1};
+  if (!col_ok || i >= a.budget) return m;
+  const int64_t src_row = kp[i];
+  if (src_row < 0 || src_row >= n_tokens) return m;
+  const int64_t sp = page_of(sbt, n_src, src_row, a.num_pages);
+  const int64_t dp = page_of(dbt, n_dst, i, a.num_pages);
+  if (sp < 0 || dp < 0) return m;
+  const int64_t so = sp * a.page_stride_bytes + (src_row & (kBlockSize - 1)) * a.row_bytes + word_off;
+  const int64_t dof = dp * a.page_stride_bytes + (i & (kBlockSize - 1)) * a.row_bytes + word_off;
+  if (so == dof) return m;
+  m.src = so;
+  m.dst = dof;
+  return m;
+}
+
 template <typename Chunk>
-__global__ __launch_bounds__(kCopyThreads) void compact_kernel(CompactArgs a) {
+__global__ __launch_bounds__(kCopyThreads) void compact_private_kernel(CompactArgs a) {
   const int b = blockIdx.y;
-  const int layer = blockIdx.z >> 1;
-  const bool is_v = (blockIdx.z & 1) != 0;
-  char* base = reinterpret_cast<char*>(is_v ? a.v_ptrs[layer] : a.k_ptrs[layer]);
-
-  const int64_t* sbt = a.src_ids + a.src_off[b];
-  const int64_t n_src = a.src_off[b + 1] - a.src_off[b];
-  const int64_t* dbt = a.inplace ? sbt : a.dst_ids + a.dst_off[b];
-  const int64_t n_dst = a.inplace ? n_src : a.dst_off[b + 1] - a.dst_off[b];
-  const int64_t* kp = a.keep + static_cast<int64_t>(b) * a.keep_stride;
-  const int64_t n_tokens = a.seq_lens[b];
-
-  const int slice_w = 1 << a.slice_shift;  // chunks per slice (divides kCopyThreads)
+  const int slice = blockIdx.x % a.n_slices;
+  const int tile = blockIdx.x / a.n_slices;
+  const int slice_w = 1 << a.slice_shift;
   const int rows_per_step = kCopyThreads >> a.slice_shift;
   const int tile_rows = rows_per_step * kCopyUnroll;
   const int col = threadIdx.x & (slice_w - 1);
   const int row_lane = threadIdx.x >> a.slice_shift;
-
-  int slice, first_tile, last_tile;
-  if (a.inplace) {
-    slice = blockIdx.x;
-    first_tile = 0;
-    last_tile = (a.budget + tile_rows - 1) / tile_rows;
-  } else {
-    slice = blockIdx.x % a.n_slices;
-    first_tile = blockIdx.x / a.n_slices;
-    last_tile = first_tile + 1;
-  }
   const int64_t chunk = static_cast<int64_t>(slice) * slice_w + col;
   const bool col_ok = chunk < a.row_chunks;
+  const int64_t word_off = chunk * static_cast<int64_t>(sizeof(Chunk));
 
-  for (int tile = first_tile; tile < last_tile; ++tile) {
-    Chunk v[kCopyUnroll];
-    int64_t dst_off[kCopyUnroll];
+  const int64_t* sbt = a.src_ids + a.src_off[b];
+  const int64_t n_src = a.src_off[b + 1] - a.src_off[b];
+  const int64_t* dbt = a.dst_ids + a.dst_off[b];
+  const int64_t n_dst = a.dst_off[b + 1] - a.dst_off[b];
+  const int64_t* kp = a.keep + static_cast<int64_t>(b) * a.keep_stride;
+  const int64_t n_tokens = a.seq_lens[b];
+
+  RowMove mv[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = static_cast<int64_t>(tile) * tile_rows + u * rows_per_step + row_lane;
+    mv[u] = resolve_row(a, sbt, n_src, dbt, n_dst, kp, n_tokens, i, word_off, col_ok);
+  }
+
+  for (int layer = 0; layer < a.n_layers; ++layer) {
+    char* kb = reinterpret_cast<char*>(a.k_ptrs[layer]);
+    char* vb = reinterpret_cast<char*>(a.v_ptrs[layer]);
+    Chunk kv[kCopyUnroll], vv[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      if (mv[u].src >= 0) {
+        kv[u] = *reinterpret_cast<const Chunk*>(kb + mv[u].src);
+        vv[u] = *reinterpret_cast<const Chunk*>(vb + mv[u].src);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      if (mv[u].src >= 0) {
+        *reinterpret_cast<Chunk*>(kb + mv[u].dst) = kv[u];
+        *reinterpret_cast<Chunk*>(vb + mv[u].dst) = vv[u];
+      }
+    }
+  }
+}
+
+template <typename Chunk>
+__global__ __launch_bounds__(kCopyThreads) void compact_inplace_kernel(CompactArgs a) {
+  const int b = blockIdx.y;
+  const int layer = blockIdx.z;
+  const int slice = blockIdx.x;
+  char* kb = reinterpret_cast<char*>(a.k_ptrs[layer]);
+  char* vb = reinterpret_cast<char*>(a.v_ptrs[layer]);
+  const int slice_w = 1 << a.slice_shift;
+  const int rows_per_step = kCopyThreads >> a.slice_shift;
+  const int tile_rows = rows_per_step * kCopyUnroll;
+  const int col = threadIdx.x & (slice_w - 1);
+  const int row_lane = threadIdx.x >> a.slice_shift;
+  const int64_t chunk = static_cast<int64_t>(slice) * slice_w + col;
+  const bool col_ok = chunk < a.row_chunks;
+  const int64_t word_off = chunk * static_cast<int64_t>(sizeof(Chunk));
+
+  const int64_t* sbt = a.src_ids + a.src_off[b];
+  const int64_t n_src = a.src_off[b + 1] - a.src_off[b];
+  const int64_t* kp = a.keep + static_cast<int64_t>(b) * a.keep_stride;
+  const int64_t n_tokens = a.seq_lens[b];
+  const int n_tiles = (a.budget + tile_rows - 1) / tile_rows;
+
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    RowMove mv[kCopyUnroll];
+    Chunk kv[kCopyUnroll], vv[kCopyUnroll];
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       const int64_t i = static_cast<int64_t>(tile) * tile_rows + u * rows_per_step + row_lane;
-      dst_off[u] = -1;
-      if (!col_ok || i >= a.budget) continue;
-      const int64_t src_row = kp[i];
-      if (src_row < 0 || src_row >= n_tokens) continue;
-      const int64_t sp = page_of(sbt, n_src, src_row, a.num_pages);
-      const int64_t dp = page_of(dbt, n_dst, i, a.num_pages);
-      if (sp < 0 || dp < 0) continue;
-      const int64_t so = sp * a.page_stride_bytes + (src_row & (kBlockSize - 1)) * a.row_bytes;
-      const int64_t dof = dp * a.page_stride_bytes + (i & (kBlockSize - 1)) * a.row_bytes;
-      if (so == dof) continue;  // row already in place
-      v[u] = *reinterpret_cast<const Chunk*>(base + so + chunk * sizeof(Chunk));
-      dst_off[u] = dof;
+      mv[u] = resolve_row(a, sbt, n_src, sbt, n_src, kp, n_tokens, i, word_off, col_ok);
+      if (mv[u].src >= 0) {
+        kv[u] = *reinterpret_cast<const Chunk*>(kb + mv[u].src);
+        vv[u] = *reinterpret_cast<const Chunk*>(vb + mv[u].src);
+      }
     }
-    if (a.inplace) {
-      // Every load of this tile has returned before any lane stores.
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-    }
+    // Every load of this tile has returned before any lane stores.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
-      if (dst_off[u] >= 0)
-        *reinterpret_cast<Chunk*>(base + dst_off[u] + chunk * sizeof(Chunk)) = v[u];
+      if (mv[u].src >= 0) {
+        *reinterpret_cast<Chunk*>(kb + mv[u].dst) = kv[u];
+        *reinterpret_cast<Chunk*>(vb + mv[u].dst) = vv[u];
+      }
     }
   }
 }
@@ -202,7 +264,7 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
                            const int64_t* src_block_offsets, const int64_t* src_block_ids,
                            const int64_t* dst_block_offsets, const int64_t* dst_block_ids,
                            const int64_t* keep, int64_t keep_stride, int budget) {
-  if (n_layers <= 0 || n_layers > 32767 || n_seq <= 0 || n_seq > 65535)
+  if (n_layers <= 0 || n_layers > 65535 || n_seq <= 0 || n_seq > 65535)
     return fail(KVC_EINVAL, "kvc_compact: bad layer or sequence count");
   if (elem_bytes != 2) return fail(KVC_EINVAL, "kvc_compact: elem_bytes must be 2");
   if (row_elems <= 0 || budget <= 0 || keep_stride < budget || num_pages <= 0)
@@ -218,10 +280,10 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   CompactArgs ca;
   ca.k_ptrs = k_layer_ptrs;
   ca.v_ptrs = v_layer_ptrs;
+  ca.n_layers = n_layers;
   ca.num_pages = num_pages;
   ca.page_stride_bytes = page_stride * elem_bytes;
   ca.row_bytes = row_elems * elem_bytes;
-  ca.inplace = inplace ? 1 : 0;
   ca.budget = budget;
   ca.seq_lens = seq_lens;
   ca.src_off = src_block_offsets;
@@ -246,17 +308,26 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   ca.n_slices = static_cast<int>(ceil_div(ca.row_chunks, int64_t(1) << shift));
   const int rows_per_step = kCopyThreads >> shift;
   const int tile_rows = rows_per_step * kCopyUnroll;
-  ca.n_row_tiles = static_cast<int>(ceil_div(budget, tile_rows));
-  const int64_t gx = inplace ? ca.n_slices : static_cast<int64_t>(ca.n_slices) * ca.n_row_tiles;
-  if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
-  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n_seq),
-            static_cast<unsigned>(2 * n_layers));
+  const int64_t n_row_tiles = ceil_div(budget, tile_rows);
   hipStream_t st = as_stream(stream);
-  switch (word) {
-    case 16: compact_kernel<uint4><<<grid, kCopyThreads, 0, st>>>(ca); break;
-    case 8: compact_kernel<uint2><<<grid, kCopyThreads, 0, st>>>(ca); break;
-    case 4: compact_kernel<uint32_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
-    default: compact_kernel<uint16_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+  if (inplace) {
+    dim3 grid(static_cast<unsigned>(ca.n_slices), static_cast<unsigned>(n_seq), static_cast<unsigned>(n_layers));
+    switch (word) {
+      case 16: compact_inplace_kernel<w128><<<grid, kCopyThreads, 0, st>>>(ca); break;
+      case 8: compact_inplace_kernel<w64><<<grid, kCopyThreads, 0, st>>>(ca); break;
+      case 4: compact_inplace_kernel<uint32_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+      default: compact_inplace_kernel<uint16_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+    }
+  } else {
+    const int64_t gx = n_row_tiles * ca.n_slices;
+    if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
+    dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n_seq));
+    switch (word) {
+      case 16: compact_private_kernel<w128><<<grid, kCopyThreads, 0, st>>>(ca); break;
+      case 8: compact_private_kernel<w64><<<grid, kCopyThreads, 0, st>>>(ca); break;
+      case 4: compact_private_kernel<uint32_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+      default: compact_private_kernel<uint16_t><<<grid, kCopyThreads, 0, st>>>(ca); break;
+    }
   }
   return launch_status("kvc_compact");
 }

@@ -427,13 +427,32 @@ struct AggArgs {
   float* agg;
 };
 
-__global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
-  __shared__ float s_mean[kAggMaxStats];
-  __shared__ float s_scale[kAggMaxStats];
-  const int b = blockIdx.y;
-  const int n = a.seq_lens[b];
-  const int t = blockIdx.x * kAggThreads + threadIdx.x;
-  if (static_cast<int64_t>(blockIdx.x) * kAggThreads >= n) return;
+__device__ __forceinline__ float normalise(float s, float mean, float scale, bool rsqrt_form) {
+  return rsqrt_form ? (s - mean) * scale : (s - mean) / scale;
+}
+
+__device__ __forceinline__ float combine_layers(float total, float best, int l, const AggArgs& a,
+                                                int64_t tok) {
+  if (l == 0) {
+    if (a.flags & KVC_AGG_ACCUMULATE) {
+      const float prev = a.agg[tok];
+      return (a.layer_mode == KVC_LAYER_MEAN) ? prev + best : max_nan(prev, best);
+    }
+    return best;
+  }
+  return (a.layer_mode == KVC_LAYER_MEAN) ? total + best : max_nan(total, best);
+}
+
+__device__ __forceinline__ float finalize(float total, const AggArgs& a) {
+  if (a.flags & KVC_AGG_FINALIZE) {
+    if (a.layer_mode == KVC_LAYER_MEAN) total = total / static_cast<float>(a.n_layers);
+    if (total != total) total = -INFINITY;
+    else if (total == INFINITY) total = 1e30f;
+  }
+  return total;
+}
+
+__device__ void load_layer_stats(const AggArgs& a, int b, float* s_mean, float* s_scale) {
   const int n_stats = a.n_layers * a.n_heads;
   const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
   for (int i = threadIdx.x; i < n_stats; i += kAggThreads) {
@@ -443,36 +462,86 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
     s_mean[i] = a.mean[si];
     s_scale[i] = rsqrt_form ? rsqrtf(v) : sqrtf(v);
   }
+}
+
+// Generic strides: one thread per token reads its heads directly.
+__global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
+  __shared__ float s_mean[kAggMaxStats];
+  __shared__ float s_scale[kAggMaxStats];
+  const int b = blockIdx.y;
+  const int n = a.seq_lens[b];
+  const int t = blockIdx.x * kAggThreads + threadIdx.x;
+  if (static_cast<int64_t>(blockIdx.x) * kAggThreads >= n) return;
+  load_layer_stats(a, b, s_mean, s_scale);
   __syncthreads();
   if (t >= n) return;
+  const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
   const int64_t tok = a.token_offsets[b] + t;
   float total = 0.0f;
   for (int l = 0; l < a.n_layers; ++l) {
     const float* row = a.raw + l * a.raw_layer_stride + tok * a.raw_token_stride;
-    float best = -INFINITY;
+    float best = 0.0f;
     for (int h = 0; h < a.n_heads; ++h) {
-      const float s = row[h * a.raw_head_stride];
       const int i = l * a.n_heads + h;
-      const float z = rsqrt_form ? (s - s_mean[i]) * s_scale[i] : (s - s_mean[i]) / s_scale[i];
+      const float z = normalise(row[h * a.raw_head_stride], s_mean[i], s_scale[i], rsqrt_form);
       best = (h == 0) ? z : max_nan(best, z);
     }
-    if (l == 0) {
-      if (a.flags & KVC_AGG_ACCUMULATE) {
-        const float prev = a.agg[tok];
-        total = (a.layer_mode == KVC_LAYER_MEAN) ? prev + best : max_nan(prev, best);
-      } else {
-        total = best;
+    total = combine_layers(total, best, l, a, tok);
+  }
+  a.agg[tok] = finalize(total, a);
+}
+
+// Token-major scores (head stride 1, token stride n_heads): each layer's block
+// of kAggThreads tokens is one contiguous span, read with coalesced loads into
+// a padded LDS tile, then every thread reduces its own token's heads.
+constexpr size_t kAggDenseMaxLds = 64 * 1024;
+
+size_t aggregate_dense_lds(int n_layers, int n_heads) {
+  return (static_cast<size_t>(2) * n_layers * n_heads + static_cast<size_t>(kAggThreads) * (n_heads + 1)) *
+         sizeof(float);
+}
+
+__global__ __launch_bounds__(kAggThreads) void aggregate_dense_kernel(AggArgs a) {
+  // Dynamic LDS: [n_layers*n_heads] means, [n_layers*n_heads] scales, then the
+  // [kAggThreads][n_heads+1] score tile (one float of padding per row keeps
+  // the per-token reads free of bank conflicts).
+  extern __shared__ float dyn[];
+  float* s_mean = dyn;
+  float* s_scale = dyn + a.n_layers * a.n_heads;
+  float* tile = s_scale + a.n_layers * a.n_heads;
+  const int b = blockIdx.y;
+  const int n = a.seq_lens[b];
+  const int t0 = blockIdx.x * kAggThreads;
+  if (t0 >= n) return;
+  const int n_tok = min(kAggThreads, n - t0);
+  const int hq = a.n_heads;
+  const int pitch = hq + 1;
+  load_layer_stats(a, b, s_mean, s_scale);
+  const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
+  const int64_t tok0 = a.token_offsets[b] + t0;
+  const int64_t tok = tok0 + threadIdx.x;
+  float total = 0.0f;
+  for (int l = 0; l < a.n_layers; ++l) {
+    const float* block = a.raw + l * a.raw_layer_stride + tok0 * hq;
+    const int n_vals = n_tok * hq;
+    __syncthreads();  // previous layer's tile fully consumed (and stats staged)
+    for (int e = threadIdx.x; e < n_vals; e += kAggThreads) {
+      const int r = e / hq;
+      tile[r * pitch + (e - r * hq)] = block[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < n_tok) {
+      const float* row = tile + threadIdx.x * pitch;
+      float best = 0.0f;
+      for (int h = 0; h < hq; ++h) {
+        const int i = l * hq + h;
+        const float z = normalise(row[h], s_mean[i], s_scale[i], rsqrt_form);
+        best = (h == 0) ? z : max_nan(best, z);
       }
-    } else {
-      total = (a.layer_mode == KVC_LAYER_MEAN) ? total + best : max_nan(total, best);
+      total = combine_layers(total, best, l, a, tok);
     }
   }
-  if (a.flags & KVC_AGG_FINALIZE) {
-    if (a.layer_mode == KVC_LAYER_MEAN) total = total / static_cast<float>(a.n_layers);
-    if (total != total) total = -INFINITY;
-    else if (total == INFINITY) total = 1e30f;
-  }
-  a.agg[tok] = total;
+  if (threadIdx.x < n_tok) a.agg[tok] = finalize(total, a);
 }
 
 template <typename Tag, bool IL>
@@ -691,6 +760,11 @@ extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int
   aa.stats_seq_stride = stats_seq_stride;
   aa.agg = agg;
   dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggThreads)), static_cast<unsigned>(n_seq));
-  aggregate_kernel<<<grid, kAggThreads, 0, as_stream(stream)>>>(aa);
+  const size_t lds = aggregate_dense_lds(n_layers, n_heads);
+  const bool dense = raw_head_stride == 1 && raw_token_stride == n_heads && lds <= kAggDenseMaxLds;
+  if (dense)
+    aggregate_dense_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
+  else
+    aggregate_kernel<<<grid, kAggThreads, 0, as_stream(stream)>>>(aa);
   return launch_status("kvc_aggregate");
 }
