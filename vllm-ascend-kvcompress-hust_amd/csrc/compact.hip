@@ -29,8 +29,21 @@
 namespace kvc {
 namespace {
 
+#ifndef KVC_COPY_UNROLL
+#define KVC_COPY_UNROLL 8
+#endif
+#ifndef KVC_COPY_NT_LOAD
+#define KVC_COPY_NT_LOAD 1
+#endif
+#ifndef KVC_COPY_NT_STORE
+#define KVC_COPY_NT_STORE 1
+#endif
+#ifndef KVC_COPY_LAYER_MAJOR
+#define KVC_COPY_LAYER_MAJOR 0
+#endif
+
 constexpr int kCopyThreads = 256;
-constexpr int kCopyUnroll = 8;  // rows per thread per tile
+constexpr int kCopyUnroll = KVC_COPY_UNROLL;  // rows per thread per tile
 
 // Native vector words (the HIP_vector_type structs would be kept in scratch).
 typedef uint32_t w128 __attribute__((ext_vector_type(4)));
@@ -55,6 +68,20 @@ struct CompactArgs {
   const int64_t* keep;
   int64_t keep_stride;
 };
+
+// Streaming word access; the non-temporal forms mark lines for early eviction.
+template <typename Chunk>
+__device__ __forceinline__ Chunk load_word(const char* p) {
+  if (KVC_COPY_NT_LOAD) return __builtin_nontemporal_load(reinterpret_cast<const Chunk*>(p));
+  return *reinterpret_cast<const Chunk*>(p);
+}
+template <typename Chunk>
+__device__ __forceinline__ void store_word(char* p, Chunk v) {
+  if (KVC_COPY_NT_STORE)
+    __builtin_nontemporal_store(v, reinterpret_cast<Chunk*>(p));
+  else
+    *reinterpret_cast<Chunk*>(p) = v;
+}
 
 __device__ __forceinline__ int64_t page_of(const int64_t* table, int64_t n_entries, int64_t row,
                                            int64_t num_pages) {
@@ -124,16 +151,60 @@ __global__ __launch_bounds__(kCopyThreads) void compact_private_kernel(CompactAr
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       if (mv[u].src >= 0) {
-        kv[u] = *reinterpret_cast<const Chunk*>(kb + mv[u].src);
-        vv[u] = *reinterpret_cast<const Chunk*>(vb + mv[u].src);
+        kv[u] = load_word<Chunk>(kb + mv[u].src);
+        vv[u] = load_word<Chunk>(vb + mv[u].src);
       }
     }
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       if (mv[u].src >= 0) {
-        *reinterpret_cast<Chunk*>(kb + mv[u].dst) = kv[u];
-        *reinterpret_cast<Chunk*>(vb + mv[u].dst) = vv[u];
+        store_word<Chunk>(kb + mv[u].dst, kv[u]);
+        store_word<Chunk>(vb + mv[u].dst, vv[u]);
       }
+    }
+  }
+}
+
+// Layer-major private variant: one workgroup per (row tile, sequence, layer);
+// the workgroups resident at any moment share one layer's pages.
+template <typename Chunk>
+__global__ __launch_bounds__(kCopyThreads) void compact_private_layer_kernel(CompactArgs a) {
+  const int b = blockIdx.y;
+  const int layer = blockIdx.z;
+  const int slice = blockIdx.x % a.n_slices;
+  const int tile = blockIdx.x / a.n_slices;
+  const int slice_w = 1 << a.slice_shift;
+  const int rows_per_step = kCopyThreads >> a.slice_shift;
+  const int tile_rows = rows_per_step * kCopyUnroll;
+  const int col = threadIdx.x & (slice_w - 1);
+  const int row_lane = threadIdx.x >> a.slice_shift;
+  const int64_t chunk = static_cast<int64_t>(slice) * slice_w + col;
+  const bool col_ok = chunk < a.row_chunks;
+  const int64_t word_off = chunk * static_cast<int64_t>(sizeof(Chunk));
+  const int64_t* sbt = a.src_ids + a.src_off[b];
+  const int64_t n_src = a.src_off[b + 1] - a.src_off[b];
+  const int64_t* dbt = a.dst_ids + a.dst_off[b];
+  const int64_t n_dst = a.dst_off[b + 1] - a.dst_off[b];
+  const int64_t* kp = a.keep + static_cast<int64_t>(b) * a.keep_stride;
+  const int64_t n_tokens = a.seq_lens[b];
+  char* kb = reinterpret_cast<char*>(a.k_ptrs[layer]);
+  char* vb = reinterpret_cast<char*>(a.v_ptrs[layer]);
+  RowMove mv[kCopyUnroll];
+  Chunk kv[kCopyUnroll], vv[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    const int64_t i = static_cast<int64_t>(tile) * tile_rows + u * rows_per_step + row_lane;
+    mv[u] = resolve_row(a, sbt, n_src, dbt, n_dst, kp, n_tokens, i, word_off, col_ok);
+    if (mv[u].src >= 0) {
+      kv[u] = load_word<Chunk>(kb + mv[u].src);
+      vv[u] = load_word<Chunk>(vb + mv[u].src);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u) {
+    if (mv[u].src >= 0) {
+      store_word<Chunk>(kb + mv[u].dst, kv[u]);
+      store_word<Chunk>(vb + mv[u].dst, vv[u]);
     }
   }
 }
@@ -321,6 +392,16 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   } else {
     const int64_t gx = n_row_tiles * ca.n_slices;
     if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
+    if (KVC_COPY_LAYER_MAJOR) {
+      dim3 lgrid(static_cast<unsigned>(gx), static_cast<unsigned>(n_seq), static_cast<unsigned>(n_layers));
+      switch (word) {
+        case 16: compact_private_layer_kernel<w128><<<lgrid, kCopyThreads, 0, st>>>(ca); break;
+        case 8: compact_private_layer_kernel<w64><<<lgrid, kCopyThreads, 0, st>>>(ca); break;
+        case 4: compact_private_layer_kernel<uint32_t><<<lgrid, kCopyThreads, 0, st>>>(ca); break;
+        default: compact_private_layer_kernel<uint16_t><<<lgrid, kCopyThreads, 0, st>>>(ca); break;
+      }
+      return launch_status("kvc_compact");
+    }
     dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n_seq));
     switch (word) {
       case 16: compact_private_kernel<w128><<<grid, kCopyThreads, 0, st>>>(ca); break;

@@ -64,9 +64,9 @@ bool make_shape(ScoreShape* s, int n_layers, int kv_heads, int head_dim, int rot
   s->units_rot = freq / 8;
   s->units = freq / 8 + pass / 16;
   int need = s->units > qpk ? s->units : qpk;
-  int shift = 0;
+  int shift = 3;  // lane groups of 8, 16 or 32 lanes
   while ((1 << shift) < need) ++shift;
-  if (shift > 6) return false;  // one head row must fit in a wave
+  if (shift > 5) return false;  // a head row must fit in 32 lanes
   s->group_shift = shift;
   // A workgroup covers every KV head of a token; groups beyond the last whole
   // token slot stay idle.
@@ -140,7 +140,7 @@ __global__ void shift_phases_kernel(int n_values, float round_start,
 // ------------------------------------------------------------- weight fold --
 
 struct FoldArgs {
-  int n_seq, n_layers, kv_heads, qpk, freq, pass, units_rot, units, rotary_dim;
+  int n_seq, n_layers, kv_heads, qpk, freq, pass, units_rot, units, rotary_dim, interleaved;
   const float* q_real;
   const float* q_imag;
   const float* scale;
@@ -152,6 +152,11 @@ struct FoldArgs {
   float* weights;  // [n_seq][n_layers][kv_heads][units][3][qpk][8]
 };
 
+// Weights are laid out in the element order of the lane's two 16-byte chunks
+// (chunk a -> W1[0..8), chunk b -> W2[0..8)), so the scorer unpacks both RoPE
+// layouts the same way; W3[j] multiplies |k| of frequency 8u+j.
+//   half:        a = re[8u..8u+8), b = im[8u..8u+8)
+//   interleaved: a = (re,im) of freqs 8u..8u+4, b = (re,im) of freqs 8u+4..8u+8
 __global__ void fold_weights_kernel(FoldArgs a) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t total = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * a.units;
@@ -169,14 +174,27 @@ __global__ void fold_weights_kernel(FoldArgs a) {
     const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
     for (int g = 0; g < a.qpk; ++g) {
       const int64_t base = (stat_row + g) * a.freq;
+      float w_re[8], w_im[8];
       for (int j = 0; j < 8; ++j) {
         const int f = unit * 8 + j;
         const float qr = a.q_real[base + f], qi = a.q_imag[base + f];
-        const float sc = a.scale[base + f], ex = a.extra[base + f];
+        const float sc = a.scale[base + f];
         const float c = pc[f], s = ps[f];
-        out[(0 * a.qpk + g) * 8 + j] = sc * (qr * c - qi * s);
-        out[(1 * a.qpk + g) * 8 + j] = sc * (qi * c + qr * s);
-        out[(2 * a.qpk + g) * 8 + j] = sc * ex;
+        w_re[j] = sc * (qr * c - qi * s);
+        w_im[j] = sc * (qi * c + qr * s);
+        out[(2 * a.qpk + g) * 8 + j] = sc * a.extra[base + f];
+      }
+      for (int e = 0; e < 8; ++e) {
+        float w1, w2;
+        if (a.interleaved) {
+          w1 = (e & 1) ? w_im[e >> 1] : w_re[e >> 1];
+          w2 = (e & 1) ? w_im[4 + (e >> 1)] : w_re[4 + (e >> 1)];
+        } else {
+          w1 = w_re[e];
+          w2 = w_im[e];
+        }
+        out[(0 * a.qpk + g) * 8 + e] = w1;
+        out[(1 * a.qpk + g) * 8 + e] = w2;
       }
     }
   } else {
@@ -210,8 +228,24 @@ struct ScoreArgs {
   double* partials;  // [n_layers][n_seq][max_tiles][kv_heads*QPK][2]
 };
 
-template <typename Tag, int QPK, bool INTERLEAVED>
+typedef uint32_t w128 __attribute__((ext_vector_type(4)));
+
+// Sum over aligned groups of GS lanes; every lane of a group ends with the
+// same bits (pairwise sums in the same association on every lane).
+template <int GS>
+__device__ __forceinline__ float group_sum_c(float v) {
+  if constexpr (GS >= 2) v += dpp_quad_xor1(v);
+  if constexpr (GS >= 4) v += dpp_quad_xor2(v);
+  if constexpr (GS >= 8) v += dpp_row_half_mirror(v);
+  if constexpr (GS >= 16) v += dpp_row_mirror(v);
+  if constexpr (GS >= 32) v += __shfl_xor(v, 16);
+  if constexpr (GS >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <typename Tag, int QPK, bool INTERLEAVED, int GS>
 __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a) {
+  constexpr int kGroupsPerWave = 64 / GS;
   const int layer = blockIdx.z;
   const int b = blockIdx.y;
   const int tile = blockIdx.x;
@@ -222,11 +256,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int gsize = 1 << a.group_shift;
-  const int groups_per_wave = 64 >> a.group_shift;
-  const int unit = lane & (gsize - 1);
-  const int gid = wave * groups_per_wave + (lane >> a.group_shift);
-  const int n_groups = (kScoreThreads / 64) * groups_per_wave;
+  const int unit = lane & (GS - 1);
+  const int gid = wave * kGroupsPerWave + lane / GS;
+  const int n_groups = (kScoreThreads / 64) * kGroupsPerWave;
   const int head = gid % a.kv_heads;
   const int tslot = gid / a.kv_heads;
   const int tpi = n_groups / a.kv_heads;  // tokens per iteration of the workgroup
@@ -283,56 +315,55 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
   float* raw_out = a.raw + layer * a.raw_layer_stride;
   const bool writer = unit < QPK && tslot < tpi;
   const int q_head = head * QPK + unit;
-
-  double sum = 0.0, sumsq = 0.0;
   const int iters = (t1 - t0 + tpi - 1) / tpi;
-  for (int k0 = 0; k0 < iters; k0 += kUnroll) {
-    uint4 ca[kUnroll], cb[kUnroll];
-    bool valid[kUnroll];
+
+  // Token group k (kUnroll iterations) <-> registers: loads are issued one
+  // group ahead of the arithmetic that consumes them.
+  auto load_group = [&](int k0, w128 (&ca)[kUnroll], w128 (&cb)[kUnroll]) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int t = t0 + tslot + (k0 + u) * tpi;
-      valid[u] = (k0 + u < iters) && (t < t1);
-      ca[u] = make_uint4(0, 0, 0, 0);
-      cb[u] = make_uint4(0, 0, 0, 0);
+      const int k = k0 + u;
+      const int t = t0 + tslot + k * tpi;
+      ca[u] = w128{0, 0, 0, 0};
+      cb[u] = w128{0, 0, 0, 0};
       const int64_t blk = t >> kBlockShift;
-      if (valid[u] && active && blk < n_blocks) {
+      if (k < iters && t < t1 && active && blk < n_blocks) {
         const int64_t page = bt[blk];
         if (page >= 0 && page < a.num_pages) {
           const uint16_t* row = kbase + page * a.page_stride +
                                 static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
-          ca[u] = *reinterpret_cast<const uint4*>(row + d1);
-          cb[u] = *reinterpret_cast<const uint4*>(row + d2);
+          ca[u] = *reinterpret_cast<const w128*>(row + d1);
+          cb[u] = *reinterpret_cast<const w128*>(row + d2);
         }
       }
     }
+  };
+
+  double sum = 0.0, sumsq = 0.0;
+  auto compute_group = [&](int k0, const w128 (&ca)[kUnroll], const w128 (&cb)[kUnroll]) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
+      const int k = k0 + u;
+      const int t = t0 + tslot + k * tpi;
       float x1[8], x2[8], x3[8];
-      const uint32_t wa[4] = {ca[u].x, ca[u].y, ca[u].z, ca[u].w};
-      const uint32_t wb[4] = {cb[u].x, cb[u].y, cb[u].z, cb[u].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (INTERLEAVED) {
-          // rotary: dword j of chunk a holds (re_j, im_j); of chunk b (re_{4+j}, im_{4+j})
-          // pass: chunk a holds dims 0..7, chunk b dims 8..15 of the unit
-          const float alo = Unpack<Tag>::lo(wa[j]), ahi = Unpack<Tag>::hi(wa[j]);
-          const float blo = Unpack<Tag>::lo(wb[j]), bhi = Unpack<Tag>::hi(wb[j]);
-          if (rotary) {
-            x1[j] = alo; x2[j] = ahi; x1[4 + j] = blo; x2[4 + j] = bhi;
-          } else {
-            x1[2 * j] = alo; x1[2 * j + 1] = ahi; x2[2 * j] = blo; x2[2 * j + 1] = bhi;
-          }
-        } else {
-          x1[2 * j] = Unpack<Tag>::lo(wa[j]);
-          x1[2 * j + 1] = Unpack<Tag>::hi(wa[j]);
-          x2[2 * j] = Unpack<Tag>::lo(wb[j]);
-          x2[2 * j + 1] = Unpack<Tag>::hi(wb[j]);
-        }
+        x1[2 * j] = Unpack<Tag>::lo(ca[u][j]);
+        x1[2 * j + 1] = Unpack<Tag>::hi(ca[u][j]);
+        x2[2 * j] = Unpack<Tag>::lo(cb[u][j]);
+        x2[2 * j + 1] = Unpack<Tag>::hi(cb[u][j]);
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float m = sqrtf(fmaf(x2[j], x2[j], x1[j] * x1[j]));
+        float re, im;
+        if (INTERLEAVED) {
+          re = j < 4 ? x1[2 * j] : x2[2 * (j - 4)];
+          im = j < 4 ? x1[2 * j + 1] : x2[2 * (j - 4) + 1];
+        } else {
+          re = x1[j];
+          im = x2[j];
+        }
+        const float m = __builtin_amdgcn_sqrtf(fmaf(im, im, re * re));
         x3[j] = rotary ? m : 0.0f;
       }
       float acc[QPK];
@@ -345,19 +376,28 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
           v = fmaf(w2[g][j], x2[j], v);
           v = fmaf(w3[g][j], x3[j], v);
         }
-        acc[g] = group_sum(v, gsize);
+        acc[g] = group_sum_c<GS>(v);
       }
       float mine = acc[0];
 #pragma unroll
       for (int g = 1; g < QPK; ++g) mine = (unit == g) ? acc[g] : mine;
-      if (valid[u] && writer) {
-        const int t = t0 + tslot + (k0 + u) * tpi;
+      if (writer && k < iters && t < t1) {
         raw_out[(tok_base + t) * a.raw_token_stride + q_head * a.raw_head_stride] = mine;
         const double dv = static_cast<double>(mine);
         sum += dv;
         sumsq = fma(dv, dv, sumsq);
       }
     }
+  };
+
+  w128 pa[kUnroll], pb[kUnroll], qa[kUnroll], qb[kUnroll];
+  load_group(0, pa, pb);
+  for (int k0 = 0; k0 < iters; k0 += 2 * kUnroll) {
+    load_group(k0 + kUnroll, qa, qb);
+    compute_group(k0, pa, pb);
+    if (k0 + kUnroll >= iters) break;
+    load_group(k0 + 2 * kUnroll, pa, pb);
+    compute_group(k0 + kUnroll, qa, qb);
   }
 
   // Combine the per-lane partial sums of each query head in a fixed order.
@@ -371,7 +411,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
     double s0 = 0.0, s1 = 0.0;
     for (int slot = 0; slot < tpi; ++slot) {
       const int gg = slot * a.kv_heads + h;  // group bound to head h, token slot `slot`
-      const int th = (gg / groups_per_wave) * 64 + (gg % groups_per_wave) * gsize + g;
+      const int th = (gg / kGroupsPerWave) * 64 + (gg % kGroupsPerWave) * GS + g;
       s0 += red[0][th];
       s1 += red[1][th];
     }
@@ -412,7 +452,7 @@ __global__ void head_stats_kernel(int n_layers, int n_seq, int n_heads, int max_
 // ---------------------------------------------------------------- aggregate --
 
 constexpr int kAggThreads = 256;
-constexpr int kAggMaxStats = 2048;  // layers * heads staged in LDS
+constexpr int kAggMaxStats = 4096;  // layers * heads staged in LDS
 
 struct AggArgs {
   int n_layers, n_heads, n_seq, layer_mode;
@@ -464,100 +504,71 @@ __device__ void load_layer_stats(const AggArgs& a, int b, float* s_mean, float* 
   }
 }
 
-// Generic strides: one thread per token reads its heads directly.
+// Four lanes per token: lane q of a token takes heads q, q+4, q+8, ...; the
+// four partial maxima meet through two DPP quad permutations.  Per-(layer,
+// head) means and scales sit in LDS.  Works for any score strides.
+constexpr int kAggLanes = 4;
+constexpr int kAggTokensPerBlock = kAggThreads / kAggLanes;
+
+__device__ __forceinline__ float quad_max_nan(float v) {
+  v = max_nan(v, dpp_quad_xor1(v));
+  v = max_nan(v, dpp_quad_xor2(v));
+  return v;
+}
+
 __global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
-  __shared__ float s_mean[kAggMaxStats];
-  __shared__ float s_scale[kAggMaxStats];
-  const int b = blockIdx.y;
-  const int n = a.seq_lens[b];
-  const int t = blockIdx.x * kAggThreads + threadIdx.x;
-  if (static_cast<int64_t>(blockIdx.x) * kAggThreads >= n) return;
-  load_layer_stats(a, b, s_mean, s_scale);
-  __syncthreads();
-  if (t >= n) return;
-  const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
-  const int64_t tok = a.token_offsets[b] + t;
-  float total = 0.0f;
-  for (int l = 0; l < a.n_layers; ++l) {
-    const float* row = a.raw + l * a.raw_layer_stride + tok * a.raw_token_stride;
-    float best = 0.0f;
-    for (int h = 0; h < a.n_heads; ++h) {
-      const int i = l * a.n_heads + h;
-      const float z = normalise(row[h * a.raw_head_stride], s_mean[i], s_scale[i], rsqrt_form);
-      best = (h == 0) ? z : max_nan(best, z);
-    }
-    total = combine_layers(total, best, l, a, tok);
-  }
-  a.agg[tok] = finalize(total, a);
-}
-
-// Token-major scores (head stride 1, token stride n_heads): each layer's block
-// of kAggThreads tokens is one contiguous span, read with coalesced loads into
-// a padded LDS tile, then every thread reduces its own token's heads.
-constexpr size_t kAggDenseMaxLds = 64 * 1024;
-
-size_t aggregate_dense_lds(int n_layers, int n_heads) {
-  return (static_cast<size_t>(2) * n_layers * n_heads + static_cast<size_t>(kAggThreads) * (n_heads + 1)) *
-         sizeof(float);
-}
-
-__global__ __launch_bounds__(kAggThreads) void aggregate_dense_kernel(AggArgs a) {
-  // Dynamic LDS: [n_layers*n_heads] means, [n_layers*n_heads] scales, then the
-  // [kAggThreads][n_heads+1] score tile (one float of padding per row keeps
-  // the per-token reads free of bank conflicts).
   extern __shared__ float dyn[];
   float* s_mean = dyn;
   float* s_scale = dyn + a.n_layers * a.n_heads;
-  float* tile = s_scale + a.n_layers * a.n_heads;
   const int b = blockIdx.y;
   const int n = a.seq_lens[b];
-  const int t0 = blockIdx.x * kAggThreads;
-  if (t0 >= n) return;
-  const int n_tok = min(kAggThreads, n - t0);
-  const int hq = a.n_heads;
-  const int pitch = hq + 1;
+  if (static_cast<int64_t>(blockIdx.x) * kAggTokensPerBlock >= n) return;
   load_layer_stats(a, b, s_mean, s_scale);
+  __syncthreads();
+  const int t = blockIdx.x * kAggTokensPerBlock + threadIdx.x / kAggLanes;
+  const int q = threadIdx.x & (kAggLanes - 1);
+  const bool valid = t < n;
   const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
-  const int64_t tok0 = a.token_offsets[b] + t0;
-  const int64_t tok = tok0 + threadIdx.x;
+  const int64_t tok = a.token_offsets[b] + (valid ? t : 0);
   float total = 0.0f;
   for (int l = 0; l < a.n_layers; ++l) {
-    const float* block = a.raw + l * a.raw_layer_stride + tok0 * hq;
-    const int n_vals = n_tok * hq;
-    __syncthreads();  // previous layer's tile fully consumed (and stats staged)
-    for (int e = threadIdx.x; e < n_vals; e += kAggThreads) {
-      const int r = e / hq;
-      tile[r * pitch + (e - r * hq)] = block[e];
-    }
-    __syncthreads();
-    if (threadIdx.x < n_tok) {
-      const float* row = tile + threadIdx.x * pitch;
-      float best = 0.0f;
-      for (int h = 0; h < hq; ++h) {
-        const int i = l * hq + h;
-        const float z = normalise(row[h], s_mean[i], s_scale[i], rsqrt_form);
-        best = (h == 0) ? z : max_nan(best, z);
+    const float* row = a.raw + l * a.raw_layer_stride + tok * a.raw_token_stride;
+    float best = -INFINITY;
+    if (valid) {
+      for (int h = q; h < a.n_heads; h += kAggLanes) {
+        const int i = l * a.n_heads + h;
+        best = max_nan(best, normalise(row[h * a.raw_head_stride], s_mean[i], s_scale[i], rsqrt_form));
       }
-      total = combine_layers(total, best, l, a, tok);
     }
+    best = quad_max_nan(best);
+    total = combine_layers(total, best, l, a, tok);
   }
-  if (threadIdx.x < n_tok) a.agg[tok] = finalize(total, a);
+  if (valid && q == 0) a.agg[tok] = finalize(total, a);
+}
+
+using ScoreKernelFn = void (*)(ScoreArgs);
+
+template <typename Tag, bool IL, int GS>
+ScoreKernelFn pick_qpk(int qpk) {
+  switch (qpk) {
+    case 1: return score_paged_kernel<Tag, 1, IL, GS>;
+    case 2: return score_paged_kernel<Tag, 2, IL, GS>;
+    case 3: return score_paged_kernel<Tag, 3, IL, GS>;
+    case 4: return score_paged_kernel<Tag, 4, IL, GS>;
+    case 5: return score_paged_kernel<Tag, 5, IL, GS>;
+    case 6: return score_paged_kernel<Tag, 6, IL, GS>;
+    case 7: return score_paged_kernel<Tag, 7, IL, GS>;
+    case 8: return score_paged_kernel<Tag, 8, IL, GS>;
+    default: return nullptr;
+  }
 }
 
 template <typename Tag, bool IL>
-using ScoreKernelFn = void (*)(ScoreArgs);
-
-template <typename Tag, bool IL>
-ScoreKernelFn<Tag, IL> pick_score_kernel(int qpk) {
-  switch (qpk) {
-    case 1: return score_paged_kernel<Tag, 1, IL>;
-    case 2: return score_paged_kernel<Tag, 2, IL>;
-    case 3: return score_paged_kernel<Tag, 3, IL>;
-    case 4: return score_paged_kernel<Tag, 4, IL>;
-    case 5: return score_paged_kernel<Tag, 5, IL>;
-    case 6: return score_paged_kernel<Tag, 6, IL>;
-    case 7: return score_paged_kernel<Tag, 7, IL>;
-    case 8: return score_paged_kernel<Tag, 8, IL>;
+ScoreKernelFn pick_group(int shift, int qpk) {
+  switch (shift) {
+    case 3: return pick_qpk<Tag, IL, 8>(qpk);
+    case 4: return pick_qpk<Tag, IL, 16>(qpk);
+    case 5: return pick_qpk<Tag, IL, 32>(qpk);
     default: return nullptr;
   }
 }
@@ -651,6 +662,7 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
   fa.units_rot = s.units_rot;
   fa.units = s.units;
   fa.rotary_dim = rotary_dim;
+  fa.interleaved = rope_style == KVC_ROPE_INTERLEAVED ? 1 : 0;
   fa.q_real = q_real;
   fa.q_imag = q_imag;
   fa.scale = freq_scale;
@@ -689,12 +701,13 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
   sa.raw_head_stride = raw_head_stride;
   sa.partials = partials;
 
-  void (*kern)(ScoreArgs) = nullptr;
+  ScoreKernelFn kern = nullptr;
   const bool il = rope_style == KVC_ROPE_INTERLEAVED;
+  const int gs = s.group_shift;
   if (dtype == KVC_DTYPE_BF16)
-    kern = il ? pick_score_kernel<Bf16Tag, true>(qpk) : pick_score_kernel<Bf16Tag, false>(qpk);
+    kern = il ? pick_group<Bf16Tag, true>(gs, qpk) : pick_group<Bf16Tag, false>(gs, qpk);
   else
-    kern = il ? pick_score_kernel<Fp16Tag, true>(qpk) : pick_score_kernel<Fp16Tag, false>(qpk);
+    kern = il ? pick_group<Fp16Tag, true>(gs, qpk) : pick_group<Fp16Tag, false>(gs, qpk);
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: qpk %d unsupported", qpk);
   dim3 grid(static_cast<unsigned>(s.max_tiles), static_cast<unsigned>(n_seq),
             static_cast<unsigned>(n_layers));
@@ -759,12 +772,8 @@ extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int
   aa.stats_layer_stride = stats_layer_stride;
   aa.stats_seq_stride = stats_seq_stride;
   aa.agg = agg;
-  dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggThreads)), static_cast<unsigned>(n_seq));
-  const size_t lds = aggregate_dense_lds(n_layers, n_heads);
-  const bool dense = raw_head_stride == 1 && raw_token_stride == n_heads && lds <= kAggDenseMaxLds;
-  if (dense)
-    aggregate_dense_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
-  else
-    aggregate_kernel<<<grid, kAggThreads, 0, as_stream(stream)>>>(aa);
+  dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggTokensPerBlock)), static_cast<unsigned>(n_seq));
+  const size_t lds = static_cast<size_t>(2) * n_layers * n_heads * sizeof(float);
+  aggregate_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
   return launch_status("kvc_aggregate");
 }
