@@ -40,7 +40,67 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--layers", type=int, default=None, help="override the materialised layer count")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument(
+        "--calibrate-copy-mib",
+        type=int,
+        default=0,
+        help="only run a plain device copy of this many MiB (3 times) to scale HBM byte counters",
+    )
+    p.add_argument(
+        "--probe-bandwidth",
+        action="store_true",
+        help="only measure streaming read / write / copy ceilings of this GPU (4 GiB buffers)",
+    )
     return p.parse_args()
+
+
+def probe_bandwidth() -> int:
+    """Achievable HBM ceilings: kvc_bandwidth_probe read / write / copy of
+    4 GiB in 16-byte words, with and without non-temporal hints, over a range
+    of grid sizes; reports the best rate of each kind in GB/s."""
+    import torch
+
+    from kvcompress_mi355x import _native
+
+    lib = _native.load()
+    size = 4 << 30
+    src = torch.empty(size, dtype=torch.uint8, device="cuda:0")
+    src.random_()
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream().cuda_stream
+    best: dict[str, float] = {}
+    detail: dict[str, float] = {}
+    for kind, name, passes in ((0, "read", 1), (1, "write", 1), (2, "copy", 2)):
+        for nt in (0, 1):
+            for blocks in (2048, 8192, 32768):
+                for _ in range(2):
+                    _native.check(lib.kvc_bandwidth_probe(stream, kind, nt, src.data_ptr(), dst.data_ptr(), size, blocks), "probe")
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(5):
+                    lib.kvc_bandwidth_probe(stream, kind, nt, src.data_ptr(), dst.data_ptr(), size, blocks)
+                end.record()
+                torch.cuda.synchronize()
+                gbs = passes * size / (start.elapsed_time(end) / 5) / 1e6
+                detail[f"{name}_nt{nt}_blocks{blocks}"] = round(gbs, 1)
+                best[name] = max(best.get(name, 0.0), round(gbs, 1))
+    print(json.dumps({"hbm_ceiling_gbs": best, "peak_gbs": HBM_PEAK_GBS, "detail": detail}), flush=True)
+    return 0
+
+
+def calibrate_copy(mib: int) -> int:
+    """A plain float32 device copy of known size, for scaling the profiler's
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 3}), flush=True)
+    return 0
 
 
 def cpu_model() -> str:
@@ -150,6 +210,10 @@ def main() -> int:
 
     from kvcompress_mi355x import workloads
 
+    if args.calibrate_copy_mib:
+        return calibrate_copy(args.calibrate_copy_mib)
+    if args.probe_bandwidth:
+        return probe_bandwidth()
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1

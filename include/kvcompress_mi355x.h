@@ -208,6 +208,16 @@ int kvc_materialize_slots(kvc_stream_t stream, void* k_cache, void* v_cache, int
                           const int64_t* src_slots, const int64_t* dst_slots, int64_t n_slots,
                           void* k_ws, void* v_ws);
 
+/* ------------------------------------------------------- measurement -- */
+
+/* Streaming HBM probe (no counterpart in the reference; used to state the
+ * achievable ceilings beside the roofline): kind 0 = read `bytes` from src
+ * (dst receives at most one word), 1 = write `bytes` to dst, 2 = copy src ->
+ * dst; 16-byte words, grid-stride over `blocks` workgroups of 256 threads,
+ * optionally with non-temporal hints.  bytes must be a multiple of 16. */
+int kvc_bandwidth_probe(kvc_stream_t stream, int kind, int nontemporal, const void* src, void* dst,
+                        int64_t bytes, int blocks);
+
 #ifdef __cplusplus
 }
 #endif

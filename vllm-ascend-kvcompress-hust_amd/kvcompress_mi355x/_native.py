@@ -62,6 +62,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_token_slots": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p]),
     "kvc_expand_block_ids": (_i32, [_p, _p, _i64, _i32, _p]),
     "kvc_materialize_slots": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _i64, _p, _p]),
+    "kvc_bandwidth_probe": (_i32, [_p, _i32, _i32, _p, _p, _i64, _i32]),
 }
 
 _LOCK = threading.Lock()
