@@ -30,66 +30,10 @@
 #include <math.h>
 #include <stdarg.h>
 
-#include "kvc_common.h"
+#include "score_internal.h"
 
 namespace kvc {
 namespace {
-
-constexpr int kScoreTile = 256;     // tokens per scoring workgroup
-constexpr int kScoreThreads = 256;  // 4 waves
-constexpr int kUnroll = 4;          // token iterations with loads in flight
-
-struct ScoreShape {
-  int n_layers, kv_heads, head_dim, rotary_dim, qpk;
-  int freq, pass, units_rot, units, group_shift;
-  int n_seq, max_tiles;
-};
-
-bool make_shape(ScoreShape* s, int n_layers, int kv_heads, int head_dim, int rotary_dim, int qpk,
-                int n_seq, int max_seq_len) {
-  if (n_layers <= 0 || kv_heads <= 0 || head_dim <= 0 || qpk <= 0 || qpk > 8 || n_seq <= 0 ||
-      max_seq_len < 0)
-    return false;
-  if (rotary_dim <= 0 || rotary_dim > head_dim || rotary_dim % 16 != 0) return false;
-  const int freq = rotary_dim / 2;
-  const int pass = head_dim - rotary_dim;
-  if (pass % 16 != 0) return false;
-  s->n_layers = n_layers;
-  s->kv_heads = kv_heads;
-  s->head_dim = head_dim;
-  s->rotary_dim = rotary_dim;
-  s->qpk = qpk;
-  s->freq = freq;
-  s->pass = pass;
-  s->units_rot = freq / 8;
-  s->units = freq / 8 + pass / 16;
-  int need = s->units > qpk ? s->units : qpk;
-  int shift = 3;  // lane groups of 8, 16 or 32 lanes
-  while ((1 << shift) < need) ++shift;
-  if (shift > 5) return false;  // a head row must fit in 32 lanes
-  s->group_shift = shift;
-  // A workgroup covers every KV head of a token; groups beyond the last whole
-  // token slot stay idle.
-  const int groups_per_wg = (kScoreThreads / 64) * (64 >> shift);
-  if (groups_per_wg < kv_heads) return false;
-  s->n_seq = n_seq;
-  s->max_tiles = static_cast<int>(ceil_div(max_seq_len, kScoreTile));
-  return true;
-}
-
-size_t weights_floats(const ScoreShape& s) {
-  return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.units * 3 * s.qpk * 8;
-}
-size_t weights_bytes_aligned(const ScoreShape& s) {
-  return (weights_floats(s) * sizeof(float) + 255) / 256 * 256;
-}
-size_t partial_count(const ScoreShape& s) {
-  return static_cast<size_t>(s.n_layers) * s.n_seq * (s.max_tiles > 0 ? s.max_tiles : 1) *
-         s.kv_heads * s.qpk;
-}
-size_t workspace_bytes(const ScoreShape& s) {
-  return weights_bytes_aligned(s) + partial_count(s) * 2 * sizeof(double);
-}
 
 // ------------------------------------------------------------- phase tables --
 
@@ -139,18 +83,7 @@ __global__ void shift_phases_kernel(int n_values, float round_start,
 
 // ------------------------------------------------------------- weight fold --
 
-struct FoldArgs {
-  int n_seq, n_layers, kv_heads, qpk, freq, pass, units_rot, units, rotary_dim, interleaved;
-  const float* q_real;
-  const float* q_imag;
-  const float* scale;
-  const float* extra;
-  const float* q_pass;
-  const float* phase_cos;
-  const float* phase_sin;
-  int64_t phase_seq_stride;
-  float* weights;  // [n_seq][n_layers][kv_heads][units][3][qpk][8]
-};
+
 
 // Weights are laid out in the element order of the lane's two 16-byte chunks
 // (chunk a -> W1[0..8), chunk b -> W2[0..8)), so the scorer unpacks both RoPE
@@ -212,21 +145,7 @@ __global__ void fold_weights_kernel(FoldArgs a) {
 
 // ----------------------------------------------------------------- scoring --
 
-struct ScoreArgs {
-  const uint64_t* k_layer_ptrs;
-  int64_t num_pages, page_stride;
-  int kv_heads, head_dim, rotary_dim, freq;
-  int units_rot, units, group_shift;
-  int n_seq, max_tiles, n_layers;
-  const int32_t* seq_lens;
-  const int64_t* token_offsets;
-  const int64_t* block_offsets;
-  const int64_t* block_ids;
-  const float* weights;
-  float* raw;
-  int64_t raw_layer_stride, raw_token_stride, raw_head_stride;
-  double* partials;  // [n_layers][n_seq][max_tiles][kv_heads*QPK][2]
-};
+
 
 typedef uint32_t w128 __attribute__((ext_vector_type(4)));
 
@@ -672,9 +591,6 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
   fa.phase_sin = phase_sin;
   fa.phase_seq_stride = phase_seq_stride;
   fa.weights = weights;
-  const int64_t fold_threads = static_cast<int64_t>(n_seq) * n_layers * kv_heads * s.units;
-  fold_weights_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 64)), 64, 0, st>>>(fa);
-  if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
 
   ScoreArgs sa;
   sa.k_layer_ptrs = k_layer_ptrs;
@@ -700,6 +616,12 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
   sa.raw_token_stride = raw_token_stride;
   sa.raw_head_stride = raw_head_stride;
   sa.partials = partials;
+
+  if (mfma_scorer_supported(s, dtype, rope_style)) return launch_mfma_scorer(st, s, fa, sa, workspace);
+
+  const int64_t fold_threads = static_cast<int64_t>(n_seq) * n_layers * kv_heads * s.units;
+  fold_weights_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 64)), 64, 0, st>>>(fa);
+  if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
 
   ScoreKernelFn kern = nullptr;
   const bool il = rope_style == KVC_ROPE_INTERLEAVED;

@@ -1,0 +1,301 @@
+// TriAttention paged-K scoring on the matrix cores (v_mfma_f32_16x16x32_bf16).
+//
+// The linear part of the score is a small GEMM per KV head: a 16-token x
+// head_dim tile of bf16 keys times head_dim x 16 folded weights (query heads of
+// the GQA group on the N axis, unused columns zero).  The keys are exact bf16
+// A operands read straight from the paged cache; the float32 weights enter as a
+// bf16 hi/lo pair (W = hi + lo to ~2^-16), so two MFMAs per 32-deep K step
+// give the float32 dot product to well inside the parity tolerance.  The
+// magnitude term sum_f W3_f |k_f| is a second GEMM over the F frequencies with
+// |k| computed in the lane (hi/lo split as well; hi*hi + hi*lo + lo*hi).
+//
+// Operand layout of v_mfma_f32_16x16x32_bf16 (checked on the device): lane l
+// holds A[l%16][8*(l/16) + e], B[8*(l/16) + e][l%16] and D[4*(l/16) + i][l%16].
+// K step j of the linear part covers head dims 32j .. 32j+31, so lane l of
+// step j reads dims 32j + 8*(l/16) .. +8 of token l%16: one 16-byte load.  With
+// half-style RoPE and F a multiple of 32, the real parts (step j < F/32) and
+// imaginary parts (step j + F/32) of frequencies 32j + 8*(l/16) + e sit in the
+// same lane, so |k| needs no data exchange and lands exactly in the layout of
+// the magnitude GEMM's A operand.
+//
+// Work split: a wave owns one KV head and walks 16-token tiles of its
+// workgroup's 256-token span; a workgroup covers hpw KV heads (hpw in {1,2,4}
+// dividing kv_heads) and 4/hpw interleaved tile streams per head.  The next
+// tile's keys are loaded before the current tile's MFMAs.  Raw scores and the
+// float64 per-tile partial sums have the same layout as the VALU scorer's, so
+// kvc_head_stats and kvc_aggregate are shared.
+
+#include "score_internal.h"
+
+namespace kvc {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Round-to-nearest-even float32 -> bf16 bits (finite inputs).
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_value(uint32_t bits) { return __uint_as_float(bits << 16); }
+
+struct MfmaGeometry {
+  int nk, nf;         // linear / magnitude K steps of 32
+  int hpw, nsub;      // KV heads per workgroup, tile streams per head
+  int head_groups;    // kv_heads / hpw
+};
+
+inline MfmaGeometry geometry(const ScoreShape& s) {
+  MfmaGeometry g;
+  g.nk = s.head_dim / 32;
+  g.nf = s.freq / 32;
+  g.hpw = (s.kv_heads % 4 == 0) ? 4 : (s.kv_heads % 2 == 0) ? 2 : 1;
+  g.nsub = 4 / g.hpw;
+  g.head_groups = s.kv_heads / g.hpw;
+  return g;
+}
+
+// ---------------------------------------------------------------- fold ------
+
+// One thread per (sequence, layer, KV head, lane): the lane's slice of every
+// fragment.  Linear weight of head dim d for query head g (tri/scoring.py:70-81,
+// 117-119 folded with the phase means):
+//   d <  F      : sqrt(fss) (qr c - qi s)     (real part, frequency d)
+//   F <= d < 2F : sqrt(fss) (qi c + qr s)     (imaginary part, frequency d-F)
+//   d >= R      : q_pass[d - R]
+// Magnitude weight of frequency f: sqrt(fss) * extra.
+__global__ void fold_mfma_kernel(FoldArgs a, int nk, int nf, uint16_t* __restrict__ frags) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * 64;
+  if (idx >= total) return;
+  const int lane = static_cast<int>(idx & 63);
+  int64_t r = idx >> 6;
+  const int head = static_cast<int>(r % a.kv_heads);
+  r /= a.kv_heads;
+  const int layer = static_cast<int>(r % a.n_layers);
+  const int b = static_cast<int>(r / a.n_layers);
+  const int g = lane & 15;
+  const int kb = lane >> 4;
+  const int n_frag = 2 * nk + 2 * nf;
+  uint16_t* out = frags + ((((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * n_frag) * 64) * 8;
+  const bool live = g < a.qpk;
+  const int64_t row = ((static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + (live ? g : 0));
+  const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
+  const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
+  const int head_dim = a.rotary_dim + a.pass;
+  for (int j = 0; j < nk; ++j) {
+    for (int e = 0; e < 8; ++e) {
+      const int d = 32 * j + 8 * kb + e;
+      float w = 0.0f;
+      if (live && d < head_dim) {
+        if (d < 2 * a.freq) {
+          const int f = d < a.freq ? d : d - a.freq;
+          const int64_t o = row * a.freq + f;
+          const float qr = a.q_real[o], qi = a.q_imag[o], sc = a.scale[o];
+          const float c = pc[f], s = ps[f];
+          w = d < a.freq ? sc * (qr * c - qi * s) : sc * (qi * c + qr * s);
+        } else {
+          w = a.q_pass[row * a.pass + (d - a.rotary_dim)];
+        }
+      }
+      const uint32_t hi = bf16_bits(w);
+      const uint32_t lo = bf16_bits(w - bf16_value(hi));
+      out[((2 * j) * 64 + lane) * 8 + e] = static_cast<uint16_t>(hi);
+      out[((2 * j + 1) * 64 + lane) * 8 + e] = static_cast<uint16_t>(lo);
+    }
+  }
+  for (int q = 0; q < nf; ++q) {
+    for (int e = 0; e < 8; ++e) {
+      const int f = 32 * q + 8 * kb + e;
+      float w = 0.0f;
+      if (live) {
+        const int64_t o = row * a.freq + f;
+        w = a.scale[o] * a.extra[o];
+      }
+      const uint32_t hi = bf16_bits(w);
+      const uint32_t lo = bf16_bits(w - bf16_value(hi));
+      out[((2 * nk + 2 * q) * 64 + lane) * 8 + e] = static_cast<uint16_t>(hi);
+      out[((2 * nk + 2 * q + 1) * 64 + lane) * 8 + e] = static_cast<uint16_t>(lo);
+    }
+  }
+}
+
+// --------------------------------------------------------------- score ------
+
+template <int NK, int NF>
+__global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, MfmaGeometry geo, int qpk,
+                                                                   const u32x4* __restrict__ frags) {
+  const int layer = blockIdx.z;
+  const int b = blockIdx.y;
+  const int tile = blockIdx.x / geo.head_groups;
+  const int hg = blockIdx.x - tile * geo.head_groups;
+  const int n = a.seq_lens[b];
+  const int t0 = tile * kScoreTile;
+  if (t0 >= n) return;  // whole workgroup leaves together
+  const int t1 = min(n, t0 + kScoreTile);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;   // A row (token in tile) / D column (query head)
+  const int kb = lane >> 4;  // K block of A/B, row block of D
+  const int head = hg * geo.hpw + wave % geo.hpw;
+  const int sub = wave / geo.hpw;
+
+  // Folded weight fragments of (sequence, layer, head).
+  constexpr int kFrags = 2 * NK + 2 * NF;
+  const u32x4* fp = frags + (((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * kFrags) * 64 + lane;
+  bf16x8 w_hi[NK], w_lo[NK], m_hi[NF], m_lo[NF];
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    w_hi[j] = __builtin_bit_cast(bf16x8, fp[(2 * j) * 64]);
+    w_lo[j] = __builtin_bit_cast(bf16x8, fp[(2 * j + 1) * 64]);
+  }
+#pragma unroll
+  for (int q = 0; q < NF; ++q) {
+    m_hi[q] = __builtin_bit_cast(bf16x8, fp[(2 * NK + 2 * q) * 64]);
+    m_lo[q] = __builtin_bit_cast(bf16x8, fp[(2 * NK + 2 * q + 1) * 64]);
+  }
+
+  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k_layer_ptrs[layer]);
+  const int64_t* bt = a.block_ids + a.block_offsets[b];
+  const int64_t n_blocks = a.block_offsets[b + 1] - a.block_offsets[b];
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * a.head_dim;
+  const int64_t lane_off = static_cast<int64_t>(head) * a.head_dim + 8 * kb;
+  const int64_t tok_base = a.token_offsets[b];
+  float* raw_out = a.raw + layer * a.raw_layer_stride;
+  const int n_mt = (t1 - t0 + 15) / 16;  // 16-token tiles in the span
+  const bool writer = r < qpk;
+  const int q_head = head * qpk + r;
+
+  auto load_tile = [&](int mt, u32x4 (&ka)[NK]) {
+    const int t = t0 + mt * 16 + r;
+    const int64_t blk = t >> kBlockShift;
+    bool ok = mt < n_mt && t < t1 && blk < n_blocks;
+    int64_t page = ok ? bt[blk] : 0;
+    ok = ok && page >= 0 && page < a.num_pages;
+    const uint16_t* row = kbase + page * a.page_stride + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
+#pragma unroll
+    for (int j = 0; j < NK; ++j) ka[j] = ok ? *reinterpret_cast<const u32x4*>(row + 32 * j) : u32x4{0, 0, 0, 0};
+  };
+
+  double sum = 0.0, sumsq = 0.0;
+  auto score_tile = [&](int mt, const u32x4 (&ka)[NK]) {
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      const bf16x8 kv = __builtin_bit_cast(bf16x8, ka[j]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_hi[j], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_lo[j], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < NF; ++q) {
+      u32x4 hi, lo;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t re_w = ka[q][w], im_w = ka[q + NF][w];
+        const float re0 = bf16_lo(re_w), re1 = bf16_hi(re_w);
+        const float im0 = bf16_lo(im_w), im1 = bf16_hi(im_w);
+        const float m0 = __builtin_amdgcn_sqrtf(fmaf(im0, im0, re0 * re0));
+        const float m1 = __builtin_amdgcn_sqrtf(fmaf(im1, im1, re1 * re1));
+        const uint32_t h0 = bf16_bits(m0), h1 = bf16_bits(m1);
+        const uint32_t l0 = bf16_bits(m0 - bf16_value(h0)), l1 = bf16_bits(m1 - bf16_value(h1));
+        hi[w] = h0 | (h1 << 16);
+        lo[w] = l0 | (l1 << 16);
+      }
+      const bf16x8 khi = __builtin_bit_cast(bf16x8, hi);
+      const bf16x8 klo = __builtin_bit_cast(bf16x8, lo);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_hi[q], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_lo[q], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, m_hi[q], acc, 0, 0, 0);
+    }
+    // D[4*kb + i][r]: token t0 + 16*mt + 4*kb + i, query head r of this KV head.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + mt * 16 + 4 * kb + i;
+      if (writer && mt < n_mt && t < t1) {
+        const float v = acc[i];
+        raw_out[(tok_base + t) * a.raw_token_stride + q_head * a.raw_head_stride] = v;
+        const double dv = static_cast<double>(v);
+        sum += dv;
+        sumsq = fma(dv, dv, sumsq);
+      }
+    }
+  };
+
+  // Tiles sub, sub + nsub, ... with the next tile's keys in flight.
+  u32x4 ka[NK], kb2[NK];
+  int mt = sub;
+  load_tile(mt, ka);
+  for (; mt < n_mt; mt += 2 * geo.nsub) {
+    load_tile(mt + geo.nsub, kb2);
+    score_tile(mt, ka);
+    if (mt + geo.nsub >= n_mt) break;
+    load_tile(mt + 2 * geo.nsub, ka);
+    score_tile(mt + geo.nsub, kb2);
+  }
+
+  // Per query head: sum the lanes of the four row blocks and the tile streams.
+  __shared__ double red[2][kScoreThreads];
+  red[0][threadIdx.x] = sum;
+  red[1][threadIdx.x] = sumsq;
+  __syncthreads();
+  const int heads_here = geo.hpw * qpk;
+  for (int i = threadIdx.x; i < heads_here; i += kScoreThreads) {
+    const int hl = i / qpk, g = i - hl * qpk;
+    double s0 = 0.0, s1 = 0.0;
+    for (int sb = 0; sb < geo.nsub; ++sb) {
+      const int w = sb * geo.hpw + hl;
+      for (int k = 0; k < 4; ++k) {
+        s0 += red[0][w * 64 + k * 16 + g];
+        s1 += red[1][w * 64 + k * 16 + g];
+      }
+    }
+    const int q = (hg * geo.hpw + hl) * qpk + g;
+    const int n_heads = a.kv_heads * qpk;
+    double* dst = a.partials + (((static_cast<int64_t>(layer) * a.n_seq + b) * a.max_tiles + tile) * n_heads + q) * 2;
+    dst[0] = s0;
+    dst[1] = s1;
+  }
+}
+
+using MfmaKernel = void (*)(ScoreArgs, MfmaGeometry, int, const u32x4*);
+
+MfmaKernel pick(int nk, int nf) {
+  switch (nk * 16 + nf) {
+    case 2 * 16 + 1: return score_mfma_kernel<2, 1>;
+    case 4 * 16 + 1: return score_mfma_kernel<4, 1>;
+    case 4 * 16 + 2: return score_mfma_kernel<4, 2>;
+    case 8 * 16 + 1: return score_mfma_kernel<8, 1>;
+    case 8 * 16 + 2: return score_mfma_kernel<8, 2>;
+    case 8 * 16 + 4: return score_mfma_kernel<8, 4>;
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+
+bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style) {
+  if (dtype != KVC_DTYPE_BF16 || rope_style != KVC_ROPE_HALF) return false;
+  if (s.head_dim % 32 != 0 || s.freq % 32 != 0 || s.qpk > 16) return false;
+  return pick(s.head_dim / 32, s.freq / 32) != nullptr;
+}
+
+int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, const FoldArgs& fa, const ScoreArgs& sa,
+                       void* weights) {
+  const MfmaGeometry geo = geometry(s);
+  MfmaKernel kern = pick(geo.nk, geo.nf);
+  if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: no MFMA scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
+  const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * 64;
+  fold_mfma_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 256)), 256, 0, stream>>>(
+      fa, geo.nk, geo.nf, static_cast<uint16_t*>(weights));
+  if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
+  const int64_t gx = static_cast<int64_t>(s.max_tiles) * geo.head_groups;
+  if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_score_paged: grid too large");
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(s.n_seq), static_cast<unsigned>(s.n_layers));
+  kern<<<grid, kScoreThreads, 0, stream>>>(sa, geo, s.qpk, static_cast<const u32x4*>(weights));
+  return launch_status("kvc_score_paged");
+}
+
+}  // namespace kvc
