@@ -41,8 +41,14 @@ namespace {
 #ifndef KVC_COPY_LAYER_MAJOR
 #define KVC_COPY_LAYER_MAJOR 0
 #endif
+#ifndef KVC_COPY_MAX_WORD
+#define KVC_COPY_MAX_WORD 16
+#endif
 
-constexpr int kCopyThreads = 256;
+#ifndef KVC_COPY_THREADS
+#define KVC_COPY_THREADS 256
+#endif
+constexpr int kCopyThreads = KVC_COPY_THREADS;
 constexpr int kCopyUnroll = KVC_COPY_UNROLL;  // rows per thread per tile
 
 // Native vector words (the HIP_vector_type structs would be kept in scratch).
@@ -53,6 +59,7 @@ struct CompactArgs {
   const uint64_t* k_ptrs;
   const uint64_t* v_ptrs;
   int n_layers;
+  int n_seq;
   int64_t num_pages;
   int64_t page_stride_bytes;
   int64_t row_bytes;
@@ -352,6 +359,7 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   ca.k_ptrs = k_layer_ptrs;
   ca.v_ptrs = v_layer_ptrs;
   ca.n_layers = n_layers;
+  ca.n_seq = n_seq;
   ca.num_pages = num_pages;
   ca.page_stride_bytes = page_stride * elem_bytes;
   ca.row_bytes = row_elems * elem_bytes;
@@ -365,7 +373,7 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   ca.keep_stride = keep_stride;
 
   // Widest word that divides both the row and the page stride.
-  int word = 16;
+  int word = KVC_COPY_MAX_WORD;
   while (word > 2 && ((ca.row_bytes % word) != 0 || (ca.page_stride_bytes % word) != 0)) word >>= 1;
   ca.row_chunks = ca.row_bytes / word;
 

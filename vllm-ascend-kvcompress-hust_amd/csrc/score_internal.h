@@ -5,7 +5,10 @@
 
 namespace kvc {
 
-constexpr int kScoreTile = 256;     // tokens per scoring workgroup
+#ifndef KVC_SCORE_TILE
+#define KVC_SCORE_TILE 256
+#endif
+constexpr int kScoreTile = KVC_SCORE_TILE;  // tokens per scoring workgroup
 constexpr int kScoreThreads = 256;  // 4 waves
 constexpr int kUnroll = 4;          // token iterations with loads in flight
 

@@ -27,12 +27,23 @@
 
 #include "score_internal.h"
 
+#ifndef KVC_MFMA_GROUP
+#define KVC_MFMA_GROUP 2  // 16-token tiles per prefetch group
+#endif
+
 namespace kvc {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Two floats -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
 
 // Round-to-nearest-even float32 -> bf16 bits (finite inputs).
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
@@ -182,12 +193,19 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
 
   double sum = 0.0, sumsq = 0.0;
   auto score_tile = [&](int mt, const u32x4 (&ka)[NK]) {
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Two independent accumulation chains keep consecutive MFMAs apart.
+    f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
       const bf16x8 kv = __builtin_bit_cast(bf16x8, ka[j]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_hi[j], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_lo[j], acc, 0, 0, 0);
+      if (j & 1) {
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_hi[j], acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_lo[j], acc1, 0, 0, 0);
+      } else {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_hi[j], acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_lo[j], acc0, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
@@ -199,17 +217,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
         const float im0 = bf16_lo(im_w), im1 = bf16_hi(im_w);
         const float m0 = __builtin_amdgcn_sqrtf(fmaf(im0, im0, re0 * re0));
         const float m1 = __builtin_amdgcn_sqrtf(fmaf(im1, im1, re1 * re1));
-        const uint32_t h0 = bf16_bits(m0), h1 = bf16_bits(m1);
-        const uint32_t l0 = bf16_bits(m0 - bf16_value(h0)), l1 = bf16_bits(m1 - bf16_value(h1));
-        hi[w] = h0 | (h1 << 16);
-        lo[w] = l0 | (l1 << 16);
+        const uint32_t h = pack_bf16(m0, m1);
+        hi[w] = h;
+        lo[w] = pack_bf16(m0 - bf16_lo(h), m1 - bf16_hi(h));
       }
       const bf16x8 khi = __builtin_bit_cast(bf16x8, hi);
       const bf16x8 klo = __builtin_bit_cast(bf16x8, lo);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_hi[q], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_lo[q], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, m_hi[q], acc, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_hi[q], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_lo[q], acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, m_hi[q], acc0, 0, 0, 0);
     }
+    const f32x4 acc = acc0 + acc1;
     // D[4*kb + i][r]: token t0 + 16*mt + 4*kb + i, query head r of this KV head.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -224,16 +242,24 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     }
   };
 
-  // Tiles sub, sub + nsub, ... with the next tile's keys in flight.
-  u32x4 ka[NK], kb2[NK];
+  // Tiles sub, sub + nsub, ... in groups of KVC_MFMA_GROUP; the next group's
+  // keys are in flight while the current group is scored.
+  constexpr int G = KVC_MFMA_GROUP;
+  u32x4 ka[G][NK], kb2[G][NK];
+  const int step = geo.nsub;
   int mt = sub;
-  load_tile(mt, ka);
-  for (; mt < n_mt; mt += 2 * geo.nsub) {
-    load_tile(mt + geo.nsub, kb2);
-    score_tile(mt, ka);
-    if (mt + geo.nsub >= n_mt) break;
-    load_tile(mt + 2 * geo.nsub, ka);
-    score_tile(mt + geo.nsub, kb2);
+#pragma unroll
+  for (int g = 0; g < G; ++g) load_tile(mt + g * step, ka[g]);
+  for (; mt < n_mt; mt += 2 * G * step) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) load_tile(mt + (G + g) * step, kb2[g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) score_tile(mt + g * step, ka[g]);
+    if (mt + G * step >= n_mt) break;
+#pragma unroll
+    for (int g = 0; g < G; ++g) load_tile(mt + (2 * G + g) * step, ka[g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) score_tile(mt + (G + g) * step, kb2[g]);
   }
 
   // Per query head: sum the lanes of the four row blocks and the tile streams.
