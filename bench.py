@@ -38,6 +38,11 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", type=int, default=2, help="workload configuration 1-5")
     p.add_argument("--layers", type=int, default=None, help="override the materialised layer count")
+    p.add_argument(
+        "--arena",
+        action="store_true",
+        help="carve every layer's K and V pool out of one allocation instead of one allocation each",
+    )
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument(
@@ -220,7 +225,7 @@ def main() -> int:
     overrides = {} if args.layers is None else {"n_layers": args.layers}
     spec = workloads.config_spec(args.config, **overrides)
     device = torch.device("cuda:0")
-    cache = workloads.build_synthetic_cache(spec, device, seed=0)
+    cache = workloads.build_synthetic_cache(spec, device, seed=0, arena=args.arena)
     pipeline, batch = workloads.build_pipeline(cache)
     torch.cuda.synchronize()
 
@@ -263,6 +268,7 @@ def main() -> int:
             "heads": f"{spec.num_attention_heads}q/{spec.num_kv_heads}kv",
             "head_dim": spec.head_dim,
             "compaction": "in-place" if spec.inplace else "private destinations",
+            "kv_pool": "one arena, per-layer K/V views" if args.arena else "one allocation per layer and K/V",
         },
         "roofline": {
             "kernel": "kvc_compact",

@@ -47,6 +47,7 @@ enum kvc_dtype { KVC_DTYPE_BF16 = 0, KVC_DTYPE_FP16 = 1 };
 enum kvc_rope_style { KVC_ROPE_HALF = 0, KVC_ROPE_INTERLEAVED = 1 };
 enum kvc_policy { KVC_POLICY_GLOBAL = 0, KVC_POLICY_V3 = 1 };
 enum kvc_layer_aggregation { KVC_LAYER_MEAN = 0, KVC_LAYER_MAX = 1 };
+enum kvc_raw_layout { KVC_RAW_TOKEN_MAJOR = 0, KVC_RAW_HEAD_MAJOR = 1 };
 
 /* Flags of kvc_aggregate. */
 #define KVC_AGG_ACCUMULATE 1u /* combine with the existing aggregate instead of overwriting it */
@@ -82,6 +83,18 @@ int kvc_shift_mean_phases(kvc_stream_t stream, int n_values, int64_t round_start
 /* Bytes of scratch kvc_score_paged needs for this shape. */
 size_t kvc_score_workspace_bytes(int n_layers, int kv_heads, int head_dim, int rotary_dim,
                                  int qpk, int n_seq, int max_seq_len);
+
+/* Raw-score layout that kvc_score_paged writes fastest for this shape:
+ * KVC_RAW_HEAD_MAJOR ([layer][head][token], raw_token_stride 1; the matrix-core
+ * scorer stores four consecutive tokens of a head per lane) or
+ * KVC_RAW_TOKEN_MAJOR ([layer][token][head], raw_head_stride 1; the vector
+ * scorer's lanes of one token span every head).  kvc_score_paged and
+ * kvc_aggregate accept either layout; this only names the faster one.
+ * Returns KVC_EINVAL for a shape kvc_score_paged rejects.  The reference keeps
+ * [kv_heads][qpk][max_len] per scoring layer (tri/method.py:232-240) and has
+ * no such query. */
+int kvc_score_raw_layout(int dtype, int rope_style, int kv_heads, int head_dim, int rotary_dim,
+                         int qpk);
 
 /* Raw TriAttention scores of every cached token against the calibrated query
  * centres (tri/scoring.py:23-120, device form tri/kernels.py:125-317):

@@ -63,7 +63,7 @@ def _run_and_check(spec, hip_device, *, check_layers=None):
     for b, n in enumerate(spec.seq_lens):
         out = _oracle_for(host, spec, b)
         for s_idx in range(len(spec.scoring_layers)):
-            got_raw = pipeline.raw[s_idx, offs[b] : offs[b + 1], :h_q].t()
+            got_raw = pipeline.raw_scores()[s_idx, offs[b] : offs[b + 1], :h_q].t()
             assert_scores_close(got_raw, out["raw"][s_idx].reshape(h_q, n))
             var, mean = out["stats"][s_idx]
             torch.testing.assert_close(pipeline.mean[s_idx, b].cpu(), mean.reshape(-1), rtol=1e-4, atol=1e-4)

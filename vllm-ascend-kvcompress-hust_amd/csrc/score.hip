@@ -238,6 +238,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
 
   // Token group k (kUnroll iterations) <-> registers: loads are issued one
   // group ahead of the arithmetic that consumes them.
+  SpanPages pages;
+  pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0);
+
   auto load_group = [&](int k0, w128 (&ca)[kUnroll], w128 (&cb)[kUnroll]) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -245,12 +248,11 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
       const int t = t0 + tslot + k * tpi;
       ca[u] = w128{0, 0, 0, 0};
       cb[u] = w128{0, 0, 0, 0};
-      const int64_t blk = t >> kBlockShift;
-      if (k < iters && t < t1 && active && blk < n_blocks) {
-        const int64_t page = bt[blk];
-        if (page >= 0 && page < a.num_pages) {
-          const uint16_t* row = kbase + page * a.page_stride +
-                                static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
+      if (k < iters && t < t1 && active) {
+        bool page_ok = false;
+        const uint16_t* pbase = pages.page(t - t0, &page_ok);
+        if (page_ok) {
+          const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
           ca[u] = *reinterpret_cast<const w128*>(row + d1);
           cb[u] = *reinterpret_cast<const w128*>(row + d2);
         }
@@ -465,6 +467,47 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
   if (valid && q == 0) a.agg[tok] = finalize(total, a);
 }
 
+// Head-major scores (unit token stride): one lane per token, so every load of
+// a wave reads 64 consecutive tokens of one head (256 contiguous bytes); the
+// head maximum stays in the lane.  Heads are visited in index order.
+constexpr int kAggHeadUnroll = 8;
+
+__global__ __launch_bounds__(kAggThreads) void aggregate_tokens_kernel(AggArgs a) {
+  extern __shared__ float dyn[];
+  float* s_mean = dyn;
+  float* s_scale = dyn + a.n_layers * a.n_heads;
+  const int b = blockIdx.y;
+  const int n = a.seq_lens[b];
+  if (static_cast<int64_t>(blockIdx.x) * kAggThreads >= n) return;
+  load_layer_stats(a, b, s_mean, s_scale);
+  __syncthreads();
+  const int t = blockIdx.x * kAggThreads + threadIdx.x;
+  const bool valid = t < n;
+  const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
+  const int64_t tok = a.token_offsets[b] + (valid ? t : 0);
+  float total = 0.0f;
+  for (int l = 0; l < a.n_layers; ++l) {
+    const float* col = a.raw + l * a.raw_layer_stride + tok;
+    const float* lm = s_mean + l * a.n_heads;
+    const float* ls = s_scale + l * a.n_heads;
+    float best = -INFINITY;
+    if (valid) {
+      int h = 0;
+      for (; h + kAggHeadUnroll <= a.n_heads; h += kAggHeadUnroll) {
+        float v[kAggHeadUnroll];
+#pragma unroll
+        for (int u = 0; u < kAggHeadUnroll; ++u) v[u] = col[(h + u) * a.raw_head_stride];
+#pragma unroll
+        for (int u = 0; u < kAggHeadUnroll; ++u)
+          best = max_nan(best, normalise(v[u], lm[h + u], ls[h + u], rsqrt_form));
+      }
+      for (; h < a.n_heads; ++h) best = max_nan(best, normalise(col[h * a.raw_head_stride], lm[h], ls[h], rsqrt_form));
+    }
+    total = combine_layers(total, best, l, a, tok);
+  }
+  if (valid) a.agg[tok] = finalize(total, a);
+}
+
 using ScoreKernelFn = void (*)(ScoreArgs);
 
 template <typename Tag, bool IL, int GS>
@@ -529,6 +572,18 @@ extern "C" size_t kvc_score_workspace_bytes(int n_layers, int kv_heads, int head
   ScoreShape s;
   if (!make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len)) return 0;
   return workspace_bytes(s);
+}
+
+extern "C" int kvc_score_raw_layout(int dtype, int rope_style, int kv_heads, int head_dim, int rotary_dim,
+                                    int qpk) {
+  ScoreShape s;
+  if (!make_shape(&s, 1, kv_heads, head_dim, rotary_dim, qpk, 1, 0))
+    return fail(KVC_EINVAL, "kvc_score_raw_layout: unsupported shape");
+  if (dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16)
+    return fail(KVC_EINVAL, "kvc_score_raw_layout: dtype must be bf16 or fp16");
+  if (rope_style != KVC_ROPE_HALF && rope_style != KVC_ROPE_INTERLEAVED)
+    return fail(KVC_EINVAL, "kvc_score_raw_layout: unknown rope style %d", rope_style);
+  return mfma_scorer_supported(s, dtype, rope_style) ? KVC_RAW_HEAD_MAJOR : KVC_RAW_TOKEN_MAJOR;
 }
 
 extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
@@ -694,8 +749,13 @@ extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int
   aa.stats_layer_stride = stats_layer_stride;
   aa.stats_seq_stride = stats_seq_stride;
   aa.agg = agg;
-  dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggTokensPerBlock)), static_cast<unsigned>(n_seq));
   const size_t lds = static_cast<size_t>(2) * n_layers * n_heads * sizeof(float);
+  if (raw_token_stride == 1) {
+    dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggThreads)), static_cast<unsigned>(n_seq));
+    aggregate_tokens_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
+    return launch_status("kvc_aggregate");
+  }
+  dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggTokensPerBlock)), static_cast<unsigned>(n_seq));
   aggregate_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
   return launch_status("kvc_aggregate");
 }

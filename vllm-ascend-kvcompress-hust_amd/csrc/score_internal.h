@@ -11,6 +11,44 @@ namespace kvc {
 constexpr int kScoreTile = KVC_SCORE_TILE;  // tokens per scoring workgroup
 constexpr int kScoreThreads = 256;  // 4 waves
 constexpr int kUnroll = 4;          // token iterations with loads in flight
+static_assert(kScoreTile % kBlockSize == 0, "a scoring span starts and ends on page boundaries");
+constexpr int kSpanPages = kScoreTile / kBlockSize;  // cache pages under one workgroup's span
+
+// Base addresses of the pages under a workgroup's token span [t0, t0 + kScoreTile),
+// resolved once before the token loop so that no K load waits on a block-table
+// load (vector loads complete in issue order, so a table load issued inside the
+// loop would also wait for every K load in flight before it).  A page that is
+// past the table or out of the pool reads as zeros, as before.
+struct SpanPages {
+  const uint16_t* base[kSpanPages];
+  bool ok[kSpanPages];
+
+  __device__ __forceinline__ void resolve(const uint16_t* kbase, const int64_t* bt, int64_t n_blocks,
+                                          int64_t num_pages, int64_t page_stride, int t0) {
+#pragma unroll
+    for (int i = 0; i < kSpanPages; ++i) {
+      const int64_t blk = (t0 >> kBlockShift) + i;
+      const int64_t p = blk < n_blocks ? bt[blk] : -1;
+      ok[i] = p >= 0 && p < num_pages;
+      base[i] = kbase + (ok[i] ? p : 0) * page_stride;
+    }
+  }
+  // Page of span-relative token `rel` (0 <= rel < kScoreTile); unrolled selects, no indexing.
+  __device__ __forceinline__ const uint16_t* page(int rel, bool* valid) const {
+    const int idx = rel >> kBlockShift;
+    const uint16_t* b = base[0];
+    bool v = ok[0];
+#pragma unroll
+    for (int i = 1; i < kSpanPages; ++i) {
+      if (idx == i) {
+        b = base[i];
+        v = ok[i];
+      }
+    }
+    *valid = v;
+    return b;
+  }
+};
 
 struct ScoreShape {
   int n_layers, kv_heads, head_dim, rotary_dim, qpk;

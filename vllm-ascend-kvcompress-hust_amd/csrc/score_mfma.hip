@@ -180,13 +180,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
   const bool writer = r < qpk;
   const int q_head = head * qpk + r;
 
+  SpanPages pages;
+  pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0);
+
   auto load_tile = [&](int mt, u32x4 (&ka)[NK]) {
-    const int t = t0 + mt * 16 + r;
-    const int64_t blk = t >> kBlockShift;
-    bool ok = mt < n_mt && t < t1 && blk < n_blocks;
-    int64_t page = ok ? bt[blk] : 0;
-    ok = ok && page >= 0 && page < a.num_pages;
-    const uint16_t* row = kbase + page * a.page_stride + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
+    const int rel = mt * 16 + r;
+    const int t = t0 + rel;
+    bool page_ok = false;
+    const uint16_t* pbase = pages.page(rel < kScoreTile ? rel : 0, &page_ok);
+    const bool ok = mt < n_mt && t < t1 && page_ok;
+    const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
 #pragma unroll
     for (int j = 0; j < NK; ++j) ka[j] = ok ? *reinterpret_cast<const u32x4*>(row + 32 * j) : u32x4{0, 0, 0, 0};
   };
@@ -229,15 +232,30 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     }
     const f32x4 acc = acc0 + acc1;
     // D[4*kb + i][r]: token t0 + 16*mt + 4*kb + i, query head r of this KV head.
+    // Head-major scores (unit token stride) leave the lane's four tokens
+    // adjacent: one 16-byte store, so a wave writes qpk whole 64-byte runs.
+    const int tq = t0 + mt * 16 + 4 * kb;
+    if (writer && mt < n_mt && tq < t1) {
+      float* dst = raw_out + (tok_base + tq) * a.raw_token_stride + q_head * a.raw_head_stride;
+      if (a.raw_token_stride == 1 && tq + 3 < t1 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = acc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = t0 + mt * 16 + 4 * kb + i;
-      if (writer && mt < n_mt && t < t1) {
-        const float v = acc[i];
-        raw_out[(tok_base + t) * a.raw_token_stride + q_head * a.raw_head_stride] = v;
-        const double dv = static_cast<double>(v);
-        sum += dv;
-        sumsq = fma(dv, dv, sumsq);
+        for (int i = 0; i < 4; ++i) {
+          const double dv = static_cast<double>(acc[i]);
+          sum += dv;
+          sumsq = fma(dv, dv, sumsq);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (tq + i < t1) {
+            const float v = acc[i];
+            dst[i * a.raw_token_stride] = v;
+            const double dv = static_cast<double>(v);
+            sum += dv;
+            sumsq = fma(dv, dv, sumsq);
+          }
+        }
       }
     }
   };

@@ -27,6 +27,8 @@ LAYER_MAX = 1
 AGG_ACCUMULATE = 1
 AGG_FINALIZE = 2
 AGG_RSQRT = 4
+RAW_TOKEN_MAJOR = 0
+RAW_HEAD_MAJOR = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -41,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_mean_phases": (_i32, [_p, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _p]),
     "kvc_shift_mean_phases": (_i32, [_p, _i32, _i64, _p, _p, _p, _p, _p]),
     "kvc_score_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "kvc_score_raw_layout": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "kvc_score_paged": (
         _i32,
         [

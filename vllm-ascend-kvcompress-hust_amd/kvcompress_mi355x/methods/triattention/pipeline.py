@@ -5,12 +5,16 @@ batch at once, the work the reference does per request in
 TriAttentionMethod._select_keep_indices and compress (tri/method.py:256-475):
 
   1. phase table      kvc_mean_phases      [n_seq, S, F]
-  2. score            kvc_score_paged      raw [S, sum N, H_q] + partial sums
+  2. score            kvc_score_paged      raw scores (layout below) + partial sums
   3. head statistics  kvc_head_stats       mean/var [S, n_seq, H_q]
   4. aggregate        kvc_aggregate        agg [sum N] (head max, layer mean, sanitise)
   5. select           kvc_select_keep      keep [n_seq, budget] ascending
   6. compact          kvc_compact          kept K/V rows of every layer
   7. block tables     kvc_rewrite_block_tables
+
+Raw scores are held [S, H_q, sum N] (head-major) when the matrix-core scorer
+serves the shape and [S, sum N, H_q] otherwise (kvc_score_raw_layout); the
+reference's workspace is [H_kv, qpk, max_len] per layer (tri/method.py:232-240).
 
 Everything is enqueued on the current stream; nothing synchronises.  Device
 buffers are sized once for a capacity (sequences, tokens, longest sequence)
@@ -222,7 +226,23 @@ class CompressionPipeline:
         dev_ = self.device
         self.phase_cos = torch.empty((self.max_seqs, s, self.tables.freq), dtype=torch.float32, device=dev_)
         self.phase_sin = torch.empty_like(self.phase_cos)
-        self.raw = torch.empty((s, self.max_tokens, self.n_heads), dtype=torch.float32, device=dev_)
+        layout = _native.load().kvc_score_raw_layout(
+            dev.cache_dtype_code(self.dtype),
+            dev.rope_style_code(self.tables.rope_style),
+            self.kv_heads,
+            self.head_dim,
+            self.tables.rotary_dim,
+            self.tables.qpk,
+        )
+        if layout < 0:
+            _native.check(layout, "kvc_score_raw_layout")
+        self.head_major = layout == _native.RAW_HEAD_MAJOR
+        if self.head_major:
+            # Token axis padded to 64 so every head row starts 256-byte aligned.
+            padded = -(-self.max_tokens // 64) * 64
+            self.raw = torch.empty((s, self.n_heads, padded), dtype=torch.float32, device=dev_)
+        else:
+            self.raw = torch.empty((s, self.max_tokens, self.n_heads), dtype=torch.float32, device=dev_)
         self.mean = torch.empty((s, self.max_seqs, self.n_heads), dtype=torch.float32, device=dev_)
         self.var = torch.empty_like(self.mean)
         self.agg = torch.empty(self.max_tokens, dtype=torch.float32, device=dev_)
@@ -234,6 +254,16 @@ class CompressionPipeline:
             raise ValueError("unsupported scoring shape for the MI355X kernel")
         self.workspace_bytes = int(ws)
         self.workspace = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=dev_)
+
+    def raw_strides(self) -> tuple[int, int, int]:
+        """(layer, token, head) element strides of the raw-score buffer."""
+        if self.head_major:
+            return int(self.raw.stride(0)), 1, int(self.raw.stride(1))
+        return int(self.raw.stride(0)), int(self.raw.stride(1)), 1
+
+    def raw_scores(self) -> torch.Tensor:
+        """Raw scores as a [S, tokens, H_q] view, whatever the buffer layout."""
+        return self.raw.transpose(1, 2) if self.head_major else self.raw
 
     def ensure_capacity(self, batch: Batch) -> None:
         if (
@@ -305,9 +335,7 @@ class CompressionPipeline:
             dev.ptr(self.phase_sin),
             t.n_layers * t.freq,
             dev.ptr(self.raw),
-            int(self.raw.stride(0)),
-            int(self.raw.stride(1)),
-            1,
+            *self.raw_strides(),
             dev.ptr(self.workspace),
             self.workspace_bytes,
         )
@@ -340,9 +368,7 @@ class CompressionPipeline:
             dev.ptr(batch.seq_lens),
             dev.ptr(batch.token_offsets),
             dev.ptr(self.raw),
-            int(self.raw.stride(0)),
-            int(self.raw.stride(1)),
-            1,
+            *self.raw_strides(),
             dev.ptr(self.mean),
             dev.ptr(self.var),
             int(self.mean.stride(0)),

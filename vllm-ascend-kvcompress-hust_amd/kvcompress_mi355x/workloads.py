@@ -277,8 +277,15 @@ def _page_tables(spec: WorkloadSpec, seed: int) -> tuple[int, list[list[int]], l
     return pool_logical * k, src_tables, dst_tables
 
 
-def build_synthetic_cache(spec: WorkloadSpec, device: torch.device | str, *, seed: int = 0) -> SyntheticCache:
-    """Allocate and fill every layer's K/V pool on ``device`` (seeded)."""
+def build_synthetic_cache(
+    spec: WorkloadSpec, device: torch.device | str, *, seed: int = 0, arena: bool = False
+) -> SyntheticCache:
+    """Allocate and fill every layer's K/V pool on ``device`` (seeded).
+
+    ``arena=True`` carves all layers' K and V page pools out of one allocation
+    ([K_0, V_0, K_1, V_1, ...], each a [pages, 128, kv_heads, head_dim] view);
+    ``arena=False`` allocates one tensor per layer and kind.  The data are the
+    same either way."""
     device = torch.device(device)
     num_pages, src_tables, dst_tables = _page_tables(spec, seed + 17)
     g = torch.Generator(device=device).manual_seed(seed)
@@ -292,10 +299,17 @@ def build_synthetic_cache(spec: WorkloadSpec, device: torch.device | str, *, see
         count = int(round(spec.outlier_fraction * slots))
         outlier_rows = torch.randperm(slots, generator=go)[:count].to(device)
     cg = torch.Generator().manual_seed(seed + 7)
-    for _layer in range(spec.n_layers):
+    pool = None
+    if arena:
+        pool = torch.empty((2 * spec.n_layers * num_pages,) + shape[1:], dtype=spec.dtype, device=device)
+    for layer in range(spec.n_layers):
         caches = []
-        for _kind in range(2):
-            cache = torch.empty(shape, dtype=spec.dtype, device=device)
+        for kind in range(2):
+            if pool is not None:
+                start = (2 * layer + kind) * num_pages
+                cache = pool[start : start + num_pages]
+            else:
+                cache = torch.empty(shape, dtype=spec.dtype, device=device)
             flat = cache.view(num_pages, -1)
             step = max(1, (1 << 26) // flat.shape[1])  # fill in bounded float32 chunks
             scale = None
