@@ -90,16 +90,16 @@ struct CompactArgs {
 
 // Streaming word access; the non-temporal forms mark lines for early eviction.
 template <typename Chunk>
-__device__ __forceinline__ Chunk load_word(const char* p) {
-  if (KVC_COPY_NT_LOAD) return __builtin_nontemporal_load(reinterpret_cast<const Chunk*>(p));
-  return *reinterpret_cast<const Chunk*>(p);
+__device__ __forceinline__ Chunk load_word(KVC_GLOBAL const char* p) {
+  if (KVC_COPY_NT_LOAD) return __builtin_nontemporal_load(reinterpret_cast<KVC_GLOBAL const Chunk*>(p));
+  return *reinterpret_cast<KVC_GLOBAL const Chunk*>(p);
 }
 template <typename Chunk>
-__device__ __forceinline__ void store_word(char* p, Chunk v) {
+__device__ __forceinline__ void store_word(KVC_GLOBAL char* p, Chunk v) {
   if (KVC_COPY_NT_STORE)
-    __builtin_nontemporal_store(v, reinterpret_cast<Chunk*>(p));
+    __builtin_nontemporal_store(v, reinterpret_cast<KVC_GLOBAL Chunk*>(p));
   else
-    *reinterpret_cast<Chunk*>(p) = v;
+    *reinterpret_cast<KVC_GLOBAL Chunk*>(p) = v;
 }
 
 __device__ __forceinline__ int64_t page_of(const int64_t* table, int64_t n_entries, int64_t row,
@@ -174,8 +174,8 @@ __global__ __launch_bounds__(kCopyThreads) void compact_private_kernel(CompactAr
   resolve_tile(a, b, tile, tile_rows, rows_per_step, row_lane, word_off, col_ok, mv);
 
   for (int layer = 0; layer < a.n_layers; ++layer) {
-    char* kb = reinterpret_cast<char*>(a.k_ptrs[layer]);
-    char* vb = reinterpret_cast<char*>(a.v_ptrs[layer]);
+    KVC_GLOBAL char* kb = gptr_from_int<char>(a.k_ptrs[layer]);
+    KVC_GLOBAL char* vb = gptr_from_int<char>(a.v_ptrs[layer]);
     Chunk kv[kCopyUnroll], vv[kCopyUnroll];
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
@@ -221,8 +221,8 @@ __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(Compac
   const int b = blockIdx.y;
   const int layer = blockIdx.z;
   const int slice = blockIdx.x;
-  char* kb = reinterpret_cast<char*>(a.k_ptrs[layer]);
-  char* vb = reinterpret_cast<char*>(a.v_ptrs[layer]);
+  KVC_GLOBAL char* kb = gptr_from_int<char>(a.k_ptrs[layer]);
+  KVC_GLOBAL char* vb = gptr_from_int<char>(a.v_ptrs[layer]);
   const int slice_w = 1 << a.slice_shift;
   const int rows_per_step = kInplaceThreads >> a.slice_shift;
   const int tile_rows = rows_per_step * kInplaceUnroll;
@@ -240,8 +240,8 @@ __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(Compac
 #pragma unroll
     for (int u = 0; u < kInplaceUnroll; ++u) {
       if (mv[u].src >= 0) {
-        kv[u] = *reinterpret_cast<const Chunk*>(kb + mv[u].src);
-        vv[u] = *reinterpret_cast<const Chunk*>(vb + mv[u].src);
+        kv[u] = *reinterpret_cast<KVC_GLOBAL const Chunk*>(kb + mv[u].src);
+        vv[u] = *reinterpret_cast<KVC_GLOBAL const Chunk*>(vb + mv[u].src);
       }
     }
     RowMove next[kInplaceUnroll];
@@ -252,8 +252,8 @@ __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(Compac
 #pragma unroll
     for (int u = 0; u < kInplaceUnroll; ++u) {
       if (mv[u].src >= 0) {
-        *reinterpret_cast<Chunk*>(kb + mv[u].dst) = kv[u];
-        *reinterpret_cast<Chunk*>(vb + mv[u].dst) = vv[u];
+        *reinterpret_cast<KVC_GLOBAL Chunk*>(kb + mv[u].dst) = kv[u];
+        *reinterpret_cast<KVC_GLOBAL Chunk*>(vb + mv[u].dst) = vv[u];
       }
       mv[u] = next[u];
     }

@@ -24,6 +24,26 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ------------------------------------------------------------------ device --
 
+// Global-memory (address space 1) views of device pointers.  Cache base
+// addresses arrive as integers in per-layer tables, and a pointer made from
+// an integer is generic: its loads and stores compile to flat_* instructions,
+// which also count against the scalar-memory wait counter, so the first wait
+// for a scalar load (a table entry, a kernel argument) drains every vector
+// load in flight.  global_* instructions count only against the vector one.
+#define KVC_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ KVC_GLOBAL const T* gptr(const T* p) {
+  return (KVC_GLOBAL const T*)p;
+}
+template <typename T>
+__device__ __forceinline__ KVC_GLOBAL T* gptr(T* p) {
+  return (KVC_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ KVC_GLOBAL T* gptr_from_int(uint64_t addr) {
+  return (KVC_GLOBAL T*)addr;
+}
+
 // 16-bit float words packed two per dword, low half first in memory.
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
     d2 = d1 + 8;
   }
 
-  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k_layer_ptrs[layer]);
+  KVC_GLOBAL const uint16_t* kbase = gptr_from_int<const uint16_t>(a.k_layer_ptrs[layer]);
   const int64_t* bt = a.block_ids + a.block_offsets[b];
   const int64_t n_blocks = a.block_offsets[b + 1] - a.block_offsets[b];
   const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * a.head_dim;
@@ -246,17 +246,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
     for (int u = 0; u < kUnroll; ++u) {
       const int k = k0 + u;
       const int t = t0 + tslot + k * tpi;
-      ca[u] = w128{0, 0, 0, 0};
-      cb[u] = w128{0, 0, 0, 0};
-      if (k < iters && t < t1 && active) {
-        bool page_ok = false;
-        const uint16_t* pbase = pages.page(t - t0, &page_ok);
-        if (page_ok) {
-          const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
-          ca[u] = *reinterpret_cast<const w128*>(row + d1);
-          cb[u] = *reinterpret_cast<const w128*>(row + d2);
-        }
-      }
+      // Unconditional loads from a row inside the pool (see the matrix-core
+      // scorer); lanes without a token or unit read offset 0 and are zeroed.
+      const bool live = k < iters && t < t1 && active;
+      bool page_ok = false;
+      KVC_GLOBAL const uint16_t* pbase = pages.page(live ? t - t0 : 0, &page_ok);
+      KVC_GLOBAL const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
+      const w128 va = *reinterpret_cast<KVC_GLOBAL const w128*>(row + (active ? d1 : 0));
+      const w128 vb = *reinterpret_cast<KVC_GLOBAL const w128*>(row + (active ? d2 : 0));
+      const bool ok = live && page_ok;
+      ca[u] = ok ? va : w128{0, 0, 0, 0};
+      cb[u] = ok ? vb : w128{0, 0, 0, 0};
     }
   };
 

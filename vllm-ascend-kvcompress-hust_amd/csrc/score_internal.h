@@ -20,10 +20,10 @@ constexpr int kSpanPages = kScoreTile / kBlockSize;  // cache pages under one wo
 // loop would also wait for every K load in flight before it).  A page that is
 // past the table or out of the pool reads as zeros, as before.
 struct SpanPages {
-  const uint16_t* base[kSpanPages];
+  KVC_GLOBAL const uint16_t* base[kSpanPages];
   bool ok[kSpanPages];
 
-  __device__ __forceinline__ void resolve(const uint16_t* kbase, const int64_t* bt, int64_t n_blocks,
+  __device__ __forceinline__ void resolve(KVC_GLOBAL const uint16_t* kbase, const int64_t* bt, int64_t n_blocks,
                                           int64_t num_pages, int64_t page_stride, int t0) {
 #pragma unroll
     for (int i = 0; i < kSpanPages; ++i) {
@@ -34,9 +34,9 @@ struct SpanPages {
     }
   }
   // Page of span-relative token `rel` (0 <= rel < kScoreTile); unrolled selects, no indexing.
-  __device__ __forceinline__ const uint16_t* page(int rel, bool* valid) const {
+  __device__ __forceinline__ KVC_GLOBAL const uint16_t* page(int rel, bool* valid) const {
     const int idx = rel >> kBlockShift;
-    const uint16_t* b = base[0];
+    KVC_GLOBAL const uint16_t* b = base[0];
     bool v = ok[0];
 #pragma unroll
     for (int i = 1; i < kSpanPages; ++i) {

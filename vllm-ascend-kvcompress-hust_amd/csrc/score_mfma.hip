@@ -52,6 +52,10 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 }
 __device__ __forceinline__ float bf16_value(uint32_t bits) { return __uint_as_float(bits << 16); }
 
+constexpr int kMfmaMaxHeadsPerWg = 4;            // hpw
+constexpr int kMfmaMaxQpk = 8;                   // make_shape admits qpk <= 8
+constexpr int kStageStride = kScoreTile + 4;     // floats per staged query-head row
+
 struct MfmaGeometry {
   int nk, nf;         // linear / magnitude K steps of 32
   int hpw, nsub;      // KV heads per workgroup, tile streams per head
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     m_lo[q] = __builtin_bit_cast(bf16x8, fp[(2 * NK + 2 * q + 1) * 64]);
   }
 
-  const uint16_t* kbase = reinterpret_cast<const uint16_t*>(a.k_layer_ptrs[layer]);
+  KVC_GLOBAL const uint16_t* kbase = gptr_from_int<const uint16_t>(a.k_layer_ptrs[layer]);
   const int64_t* bt = a.block_ids + a.block_offsets[b];
   const int64_t n_blocks = a.block_offsets[b + 1] - a.block_offsets[b];
   const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * a.head_dim;
@@ -178,7 +182,12 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
   float* raw_out = a.raw + layer * a.raw_layer_stride;
   const int n_mt = (t1 - t0 + 15) / 16;  // 16-token tiles in the span
   const bool writer = r < qpk;
-  const int q_head = head * qpk + r;
+  const int hl_wave = wave % geo.hpw;  // KV head slot of this wave inside the workgroup
+
+  // Score stage: [hpw][qpk][kStageStride] floats, rows padded by four floats
+  // so the query-head rows of one wave start in different LDS banks.
+  __shared__ __attribute__((aligned(16))) float stage[kMfmaMaxHeadsPerWg * kMfmaMaxQpk * kStageStride];
+  float* stage_row = stage + (hl_wave * qpk + (writer ? r : 0)) * kStageStride;
 
   SpanPages pages;
   pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0);
@@ -187,11 +196,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     const int rel = mt * 16 + r;
     const int t = t0 + rel;
     bool page_ok = false;
-    const uint16_t* pbase = pages.page(rel < kScoreTile ? rel : 0, &page_ok);
+    KVC_GLOBAL const uint16_t* pbase = pages.page(rel < kScoreTile ? rel : 0, &page_ok);
     const bool ok = mt < n_mt && t < t1 && page_ok;
-    const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
+    // Always a row inside the pool (unresolved pages read page 0), so the loads
+    // are unconditional and rows out of range are zeroed afterwards: loads under
+    // a branch would make the compiler wait for every load in flight at the join.
+    KVC_GLOBAL const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
 #pragma unroll
-    for (int j = 0; j < NK; ++j) ka[j] = ok ? *reinterpret_cast<const u32x4*>(row + 32 * j) : u32x4{0, 0, 0, 0};
+    for (int j = 0; j < NK; ++j) {
+      const u32x4 v = *reinterpret_cast<KVC_GLOBAL const u32x4*>(row + 32 * j);
+      ka[j] = ok ? v : u32x4{0, 0, 0, 0};
+    }
   };
 
   double sum = 0.0, sumsq = 0.0;
@@ -232,29 +247,19 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     }
     const f32x4 acc = acc0 + acc1;
     // D[4*kb + i][r]: token t0 + 16*mt + 4*kb + i, query head r of this KV head.
-    // Head-major scores (unit token stride) leave the lane's four tokens
-    // adjacent: one 16-byte store, so a wave writes qpk whole 64-byte runs.
-    const int tq = t0 + mt * 16 + 4 * kb;
-    if (writer && mt < n_mt && tq < t1) {
-      float* dst = raw_out + (tok_base + tq) * a.raw_token_stride + q_head * a.raw_head_stride;
-      if (a.raw_token_stride == 1 && tq + 3 < t1 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-        *reinterpret_cast<f32x4*>(dst) = acc;
+    // Scores go to the workgroup's LDS stage (four adjacent tokens per lane,
+    // one 16-byte write); global stores wait until the span is done, so the
+    // loop's waits cover only K loads (vector memory operations retire in
+    // issue order, and a store in the loop would hold up the next tile).
+    const int rel = mt * 16 + 4 * kb;
+    if (writer && mt < n_mt) {
+      *reinterpret_cast<f32x4*>(stage_row + rel) = acc;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
+        if (t0 + rel + i < t1) {
           const double dv = static_cast<double>(acc[i]);
           sum += dv;
           sumsq = fma(dv, dv, sumsq);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (tq + i < t1) {
-            const float v = acc[i];
-            dst[i * a.raw_token_stride] = v;
-            const double dv = static_cast<double>(v);
-            sum += dv;
-            sumsq = fma(dv, dv, sumsq);
-          }
         }
       }
     }
@@ -285,6 +290,34 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
   red[0][threadIdx.x] = sum;
   red[1][threadIdx.x] = sumsq;
   __syncthreads();
+
+  // Stage -> raw scores: row (hl, g) holds query head (hg*hpw + hl)*qpk + g
+  // for the span's tokens.  Head-major scores are contiguous per row (16-byte
+  // stores where aligned); token-major ones are contiguous across the rows.
+  const int span = t1 - t0;
+  const int rows = geo.hpw * qpk;
+  const int q_first = hg * geo.hpw * qpk;
+  if (a.raw_token_stride == 1) {
+    const int span4 = (span + 3) >> 2;
+    for (int idx = threadIdx.x; idx < rows * span4; idx += kScoreThreads) {
+      const int row = idx / span4;
+      const int c = (idx - row * span4) << 2;
+      const float* src = stage + row * kStageStride + c;
+      float* dst = raw_out + (tok_base + t0 + c) + static_cast<int64_t>(q_first + row) * a.raw_head_stride;
+      if (c + 3 < span && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = *reinterpret_cast<const f32x4*>(src);
+      } else {
+        for (int i = 0; i < 4 && c + i < span; ++i) dst[i] = src[i];
+      }
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < rows * span; idx += kScoreThreads) {
+      const int t = idx / rows;
+      const int row = idx - t * rows;
+      raw_out[(tok_base + t0 + t) * a.raw_token_stride + static_cast<int64_t>(q_first + row) * a.raw_head_stride] =
+          stage[row * kStageStride + t];
+    }
+  }
   const int heads_here = geo.hpw * qpk;
   for (int i = threadIdx.x; i < heads_here; i += kScoreThreads) {
     const int hl = i / qpk, g = i - hl * qpk;
@@ -322,7 +355,7 @@ MfmaKernel pick(int nk, int nf) {
 
 bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style) {
   if (dtype != KVC_DTYPE_BF16 || rope_style != KVC_ROPE_HALF) return false;
-  if (s.head_dim % 32 != 0 || s.freq % 32 != 0 || s.qpk > 16) return false;
+  if (s.head_dim % 32 != 0 || s.freq % 32 != 0 || s.qpk > kMfmaMaxQpk) return false;
   return pick(s.head_dim / 32, s.freq / 32) != nullptr;
 }
 
