@@ -6,8 +6,9 @@
 // them from the top, which pins the exact key T of the K-th largest score and
 // how many scores equal to T are still needed.  A last pass in index order
 // keeps every key > T plus the first `need` keys == T (ties go to the lowest
-// index) and writes the kept indices with wave ballots and a workgroup prefix
-// sum, so the output is sorted without a sort.
+// index): each thread owns a contiguous run of indices, and two workgroup
+// prefix sums give every run its ties and its first output slot, so the
+// output is sorted without a sort.
 //
 // Segments follow select_keep_indices (tri/selection.py:108-196): the protected
 // prefix [0, prefix) and recent window [n-recent, n) are always kept; policy
@@ -22,6 +23,7 @@ namespace {
 
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelUnroll = 4;  // float4 words per thread in flight in a histogram pass
 
 struct SelectArgs {
   int n_seq, budget, prefix, recent, segments, policy;
@@ -52,14 +54,69 @@ __device__ Segment v3_segment(int64_t ms, int64_t mc, int64_t evict, int k, int 
   return s;
 }
 
-__device__ __forceinline__ uint32_t lane_prefix(uint64_t mask, int lane) {
-  return static_cast<uint32_t>(__popcll(mask & ((1ull << lane) - 1ull)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Calls f(i, key) for every i in [start, stop), spread over the workgroup:
+// scalar head up to 16-byte alignment, float4 words kSelUnroll at a time
+// (loads issued together), scalar tail.
+template <typename F>
+__device__ __forceinline__ void for_each_key(const float* sc, int64_t start, int64_t stop, F&& f) {
+  const int tid = threadIdx.x;
+  const int64_t misalign = (reinterpret_cast<uintptr_t>(sc + start) >> 2) & 3;
+  int64_t head = (4 - misalign) & 3;
+  if (head > stop - start) head = stop - start;
+  for (int64_t i = start + tid; i < start + head; i += kSelThreads) f(i, float_key(sc[i]));
+  const int64_t body = start + head;
+  const int64_t n4 = (stop - body) >> 2;
+  const f32x4* v = reinterpret_cast<const f32x4*>(sc + body);
+  for (int64_t w0 = tid; w0 < n4; w0 += static_cast<int64_t>(kSelThreads) * kSelUnroll) {
+    f32x4 x[kSelUnroll];
+#pragma unroll
+    for (int u = 0; u < kSelUnroll; ++u) {
+      const int64_t w = w0 + static_cast<int64_t>(u) * kSelThreads;
+      x[u] = v[w < n4 ? w : n4 - 1];  // in range; surplus words are ignored below
+    }
+#pragma unroll
+    for (int u = 0; u < kSelUnroll; ++u) {
+      const int64_t w = w0 + static_cast<int64_t>(u) * kSelThreads;
+      if (w < n4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f(body + 4 * w + e, float_key(x[u][e]));
+      }
+    }
+  }
+  for (int64_t i = body + 4 * n4 + tid; i < stop; i += kSelThreads) f(i, float_key(sc[i]));
+}
+
+// Exclusive prefix sum over the workgroup (thread order); *total gets the sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t u = __shfl_up(incl, off);
+    if (lane >= off) incl += u;
+  }
+  if (lane == 63) s_wave[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSelWaves; ++w) {
+    const uint32_t t = s_wave[w];
+    if (w < wave) before += t;
+    all += t;
+  }
+  __syncthreads();  // s_wave is reused by the next scan
+  *total = all;
+  return before + incl - v;
 }
 
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
+  __shared__ uint32_t whist[kSelWaves][256];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t s_digit, s_need;
-  __shared__ uint32_t w_take[kSelWaves], w_eq[kSelWaves];
+  __shared__ uint32_t s_wave[kSelWaves];
 
   const int b = blockIdx.y;
   const int seg = blockIdx.x;
@@ -103,15 +160,24 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
   }
 
   // ---- radix select of the K-th largest key --------------------------------
+  // Each wave counts into its own LDS histogram (keys of similar scores share
+  // their high digits, so one shared histogram would serialise the atomics).
   uint32_t want = 0, mask = 0;
   uint32_t need = static_cast<uint32_t>(s.keep);
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    if (tid < 256) hist[tid] = 0;
+    for (int i = tid; i < kSelWaves * 256; i += kSelThreads) (&whist[0][0])[i] = 0;
     __syncthreads();
-    for (int64_t i = s.start + tid; i < s.stop; i += kSelThreads) {
-      const uint32_t k = float_key(sc[i]);
-      if ((k & mask) == want) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    uint32_t* mine = whist[wave];
+    for_each_key(sc, s.start, s.stop, [&](int64_t, uint32_t k) {
+      if ((k & mask) == want) atomicAdd(&mine[(k >> shift) & 255u], 1u);
+    });
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int w = 0; w < kSelWaves; ++w) c += whist[w][tid];
+      hist[tid] = c;
     }
     __syncthreads();
     if (tid < 64) {
@@ -142,40 +208,41 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
     need = s_need;
     __syncthreads();
   }
-  const uint32_t thresh = want;  // exact key of the K-th largest score
+  const uint32_t thresh = want;   // exact key of the K-th largest score
   const uint32_t need_eq = need;  // keys equal to thresh that are kept
 
   // ---- ordered emission --------------------------------------------------
-  uint32_t base_take = 0, base_eq = 0;
-  for (int64_t chunk = s.start; chunk < s.stop; chunk += kSelThreads) {
-    const int64_t i = chunk + tid;
-    const bool in = i < s.stop;
-    const uint32_t k = in ? float_key(sc[i]) : 0u;
-    const bool gt = in && k > thresh;
-    const bool eq = in && k == thresh;
-    const uint64_t m_eq = __ballot(eq);
-    if (lane == 0) w_eq[wave] = static_cast<uint32_t>(__popcll(m_eq));
-    __syncthreads();
-    uint32_t eq_before = base_eq + lane_prefix(m_eq, lane);
-    uint32_t eq_total = 0;
-    for (int w = 0; w < kSelWaves; ++w) {
-      if (w < wave) eq_before += w_eq[w];
-      eq_total += w_eq[w];
+  // Thread t owns the contiguous run [start + t*R, start + (t+1)*R): it counts
+  // its keys above and equal to the threshold, two workgroup scans give its
+  // ties to keep (the first need_eq ties in index order) and its first output
+  // slot, and it writes its kept indices in order.
+  const int64_t run = (len + kSelThreads - 1) / kSelThreads;
+  const int64_t r0 = min(s.start + tid * run, s.stop);
+  const int64_t r1 = min(r0 + run, s.stop);
+  uint32_t n_gt = 0, n_eq = 0;
+#pragma unroll 4
+  for (int64_t i = r0; i < r1; ++i) {
+    const uint32_t k = float_key(sc[i]);
+    n_gt += k > thresh;
+    n_eq += k == thresh;
+  }
+  uint32_t total;
+  const uint32_t eq_before = block_exclusive_scan(n_eq, s_wave, &total);
+  const uint32_t eq_take = eq_before >= need_eq ? 0u : min(n_eq, need_eq - eq_before);
+  uint32_t pos = block_exclusive_scan(n_gt + eq_take, s_wave, &total);
+  uint32_t eq_left = eq_take;
+#pragma unroll 4
+  for (int64_t i = r0; i < r1; ++i) {
+    const uint32_t k = float_key(sc[i]);
+    bool take = k > thresh;
+    if (k == thresh && eq_left > 0) {
+      take = true;
+      --eq_left;
     }
-    const bool take = gt || (eq && eq_before < need_eq);
-    const uint64_t m_take = __ballot(take);
-    if (lane == 0) w_take[wave] = static_cast<uint32_t>(__popcll(m_take));
-    __syncthreads();
-    uint32_t pos = base_take + lane_prefix(m_take, lane);
-    uint32_t take_total = 0;
-    for (int w = 0; w < kSelWaves; ++w) {
-      if (w < wave) pos += w_take[w];
-      take_total += w_take[w];
+    if (take) {
+      if (out_base + pos < a.budget) out[out_base + pos] = i;
+      ++pos;
     }
-    if (take && out_base + pos < a.budget) out[out_base + pos] = i;
-    base_take += take_total;
-    base_eq += eq_total;
-    __syncthreads();
   }
 }
 
