@@ -345,23 +345,33 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
 
 // --------------------------------------------------------------- head stats --
 
-__global__ void head_stats_kernel(int n_layers, int n_seq, int n_heads, int max_tiles,
-                                  const int32_t* __restrict__ seq_lens,
-                                  const double* __restrict__ partials, float* __restrict__ mean,
-                                  float* __restrict__ var) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= static_cast<int64_t>(n_layers) * n_seq * n_heads) return;
+// One wave per (layer, sequence, query head): lane l sums tiles l, l+64, ...
+// and a fixed butterfly combines the lanes, so the result is the same on
+// every run.  Population variance as torch.var_mean(correction=0).
+__global__ __launch_bounds__(256) void head_stats_kernel(int n_layers, int n_seq, int n_heads, int max_tiles,
+                                                         const int32_t* __restrict__ seq_lens,
+                                                         const double* __restrict__ partials,
+                                                         float* __restrict__ mean, float* __restrict__ var) {
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (idx >= static_cast<int64_t>(n_layers) * n_seq * n_heads) return;  // whole wave leaves together
   const int q = static_cast<int>(idx % n_heads);
   const int64_t ls = idx / n_heads;  // layer * n_seq + b
   const int b = static_cast<int>(ls % n_seq);
   const int n = seq_lens[b];
   const int tiles = static_cast<int>((n + kScoreTile - 1) / kScoreTile);
   double s0 = 0.0, s1 = 0.0;
-  for (int t = 0; t < tiles; ++t) {
+  for (int t = lane; t < tiles; t += 64) {
     const double* p = partials + ((ls * max_tiles + t) * n_heads + q) * 2;
     s0 += p[0];
     s1 += p[1];
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    s0 += __shfl_xor(s0, off);
+    s1 += __shfl_xor(s1, off);
+  }
+  if (lane != 0) return;
   const double inv_n = 1.0 / static_cast<double>(n);
   const double m = s0 * inv_n;
   double v = s1 * inv_n - m * m;
@@ -709,7 +719,7 @@ extern "C" int kvc_head_stats(kvc_stream_t stream, int n_layers, int kv_heads, i
       static_cast<const char*>(workspace) + weights_bytes_aligned(s));
   const int n_heads = kv_heads * qpk;
   const int64_t total = static_cast<int64_t>(n_layers) * n_seq * n_heads;
-  head_stats_kernel<<<static_cast<unsigned>(ceil_div(total, 64)), 64, 0, as_stream(stream)>>>(
+  head_stats_kernel<<<static_cast<unsigned>(ceil_div(total * 64, 256)), 256, 0, as_stream(stream)>>>(
       n_layers, n_seq, n_heads, s.max_tiles > 0 ? s.max_tiles : 1, seq_lens, partials, mean, var);
   return launch_status("kvc_head_stats");
 }

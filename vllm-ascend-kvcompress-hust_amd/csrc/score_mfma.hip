@@ -74,67 +74,65 @@ inline MfmaGeometry geometry(const ScoreShape& s) {
 
 // ---------------------------------------------------------------- fold ------
 
-// One thread per (sequence, layer, KV head, lane): the lane's slice of every
-// fragment.  Linear weight of head dim d for query head g (tri/scoring.py:70-81,
-// 117-119 folded with the phase means):
+// One thread per (sequence, layer, KV head, fragment, lane): the lane's eight
+// bf16 values of one fragment.  Linear weight of head dim d for query head g
+// (tri/scoring.py:70-81, 117-119 folded with the phase means):
 //   d <  F      : sqrt(fss) (qr c - qi s)     (real part, frequency d)
 //   F <= d < 2F : sqrt(fss) (qi c + qr s)     (imaginary part, frequency d-F)
 //   d >= R      : q_pass[d - R]
-// Magnitude weight of frequency f: sqrt(fss) * extra.
+// Magnitude weight of frequency f: sqrt(fss) * extra.  Fragments 2j / 2j+1
+// hold the hi / lo bf16 parts of linear step j, 2nk+2q / 2nk+2q+1 those of
+// magnitude step q.
 __global__ void fold_mfma_kernel(FoldArgs a, int nk, int nf, uint16_t* __restrict__ frags) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * 64;
+  const int n_frag = 2 * nk + 2 * nf;
+  const int64_t total = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * n_frag * 64;
   if (idx >= total) return;
   const int lane = static_cast<int>(idx & 63);
   int64_t r = idx >> 6;
+  const int frag = static_cast<int>(r % n_frag);
+  r /= n_frag;
   const int head = static_cast<int>(r % a.kv_heads);
   r /= a.kv_heads;
   const int layer = static_cast<int>(r % a.n_layers);
   const int b = static_cast<int>(r / a.n_layers);
   const int g = lane & 15;
   const int kb = lane >> 4;
-  const int n_frag = 2 * nk + 2 * nf;
-  uint16_t* out = frags + ((((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * n_frag) * 64) * 8;
   const bool live = g < a.qpk;
   const int64_t row = ((static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + (live ? g : 0));
   const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
   const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
   const int head_dim = a.rotary_dim + a.pass;
-  for (int j = 0; j < nk; ++j) {
-    for (int e = 0; e < 8; ++e) {
-      const int d = 32 * j + 8 * kb + e;
-      float w = 0.0f;
+  const bool low = (frag & 1) != 0;
+  const int step = frag >> 1;
+  uint16_t out[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float w = 0.0f;
+    if (step < nk) {
+      const int d = 32 * step + 8 * kb + e;
       if (live && d < head_dim) {
         if (d < 2 * a.freq) {
           const int f = d < a.freq ? d : d - a.freq;
           const int64_t o = row * a.freq + f;
           const float qr = a.q_real[o], qi = a.q_imag[o], sc = a.scale[o];
-          const float c = pc[f], s = ps[f];
-          w = d < a.freq ? sc * (qr * c - qi * s) : sc * (qi * c + qr * s);
+          const float c = pc[f], sn = ps[f];
+          w = d < a.freq ? sc * (qr * c - qi * sn) : sc * (qi * c + qr * sn);
         } else {
           w = a.q_pass[row * a.pass + (d - a.rotary_dim)];
         }
       }
-      const uint32_t hi = bf16_bits(w);
-      const uint32_t lo = bf16_bits(w - bf16_value(hi));
-      out[((2 * j) * 64 + lane) * 8 + e] = static_cast<uint16_t>(hi);
-      out[((2 * j + 1) * 64 + lane) * 8 + e] = static_cast<uint16_t>(lo);
+    } else if (live) {
+      const int f = 32 * (step - nk) + 8 * kb + e;
+      const int64_t o = row * a.freq + f;
+      w = a.scale[o] * a.extra[o];
     }
+    const uint32_t hi = bf16_bits(w);
+    out[e] = static_cast<uint16_t>(low ? bf16_bits(w - bf16_value(hi)) : hi);
   }
-  for (int q = 0; q < nf; ++q) {
-    for (int e = 0; e < 8; ++e) {
-      const int f = 32 * q + 8 * kb + e;
-      float w = 0.0f;
-      if (live) {
-        const int64_t o = row * a.freq + f;
-        w = a.scale[o] * a.extra[o];
-      }
-      const uint32_t hi = bf16_bits(w);
-      const uint32_t lo = bf16_bits(w - bf16_value(hi));
-      out[((2 * nk + 2 * q) * 64 + lane) * 8 + e] = static_cast<uint16_t>(hi);
-      out[((2 * nk + 2 * q + 1) * 64 + lane) * 8 + e] = static_cast<uint16_t>(lo);
-    }
-  }
+  uint16_t* dst = frags + (((((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * n_frag + frag) * 64) + lane) * 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dst[e] = out[e];
 }
 
 // --------------------------------------------------------------- score ------
@@ -364,7 +362,7 @@ int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, const FoldArgs& 
   const MfmaGeometry geo = geometry(s);
   MfmaKernel kern = pick(geo.nk, geo.nf);
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: no MFMA scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
-  const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * 64;
+  const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * (2 * geo.nk + 2 * geo.nf) * 64;
   fold_mfma_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 256)), 256, 0, stream>>>(
       fa, geo.nk, geo.nf, static_cast<uint16_t*>(weights));
   if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
