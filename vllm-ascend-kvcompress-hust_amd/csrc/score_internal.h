@@ -92,11 +92,12 @@ inline size_t weights_floats(const ScoreShape& s) {
   return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.units * 3 * s.qpk * 8;
 }
 // MFMA fragments: per (sequence, layer, KV head), 2*(head_dim/32) linear and
-// 2*(F/32) |k| fragments (bf16 hi/lo) of 64 lanes x 16 bytes.
+// 2*(F/32) |k| fragments (bf16 hi/lo), each holding the 16-byte words of the
+// 4*qpk lanes of live query heads.
 inline size_t mfma_fragment_bytes(const ScoreShape& s) {
   if (s.head_dim % 32 != 0 || s.freq % 32 != 0) return 0;
   const size_t frags = 2 * static_cast<size_t>(s.head_dim / 32) + 2 * static_cast<size_t>(s.freq / 32);
-  return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * frags * 64 * 16;
+  return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * frags * 4 * s.qpk * 16;
 }
 // The weight region holds either layout.
 inline size_t weights_bytes_aligned(const ScoreShape& s) {
