@@ -221,6 +221,39 @@ int kvc_materialize_slots(kvc_stream_t stream, void* k_cache, void* v_cache, int
                           const int64_t* src_slots, const int64_t* dst_slots, int64_t n_slots,
                           void* k_ws, void* v_ws);
 
+/* ------------------------------------------------- decode after compaction -- */
+
+/* Physical positions of tokens written after a compaction (shift_positions,
+ * tri/kernels.py:35-47; called by the slot-mapping hook pkg/provider.py:687-705):
+ *   output[i] = positions[i] - request_offsets[request_indices[i]]
+ * where request_offsets[r] = semantic length - physical length of request r
+ * (pkg/provider.py:52-54).  request_indices are int32 (index_bytes 4) or int64
+ * (index_bytes 8); positions, offsets and output are int64. */
+int kvc_shift_positions(kvc_stream_t stream, const int64_t* positions, const void* request_indices,
+                        int index_bytes, const int64_t* request_offsets, int64_t n, int64_t* output);
+
+/* Slot mapping of one step's tokens from their physical positions: the
+ * shift above fused with the host block table's compute_slot_mapping that the
+ * reference hooks (pkg/plugin.py:487-506).  Request r owns tokens
+ * [query_start_loc[r], query_start_loc[r+1]); with p = positions[i] -
+ * request_offsets[r] (request_offsets may be NULL: no shift),
+ *   slot_mapping[i] = block_table[r*block_table_stride + p/block_size]*block_size + p%block_size,
+ * or -1 when p is negative, p/block_size >= max_blocks or the table entry is
+ * negative.  Tokens in [query_start_loc[num_reqs], num_tokens) are padding and
+ * get -1.  block_table is int32 (the host's layout); physical_positions, if
+ * not NULL, receives p (positions[i] for padding). */
+int kvc_physical_slot_mapping(kvc_stream_t stream, int num_reqs, const int32_t* query_start_loc,
+                              const int64_t* positions, const int64_t* request_offsets,
+                              const int32_t* block_table, int64_t block_table_stride, int max_blocks,
+                              int block_size, int64_t num_tokens, int64_t* slot_mapping,
+                              int64_t* physical_positions);
+
+/* Physical attention lengths: seq_lens[r] -= request_offsets[r] for r < num_reqs,
+ * in place, int32 (elem_bytes 4) or int64 (elem_bytes 8) lengths (device half of
+ * apply_physical_attention_lengths, pkg/provider.py:707-728). */
+int kvc_shift_lengths(kvc_stream_t stream, void* seq_lens, int elem_bytes, const int64_t* request_offsets,
+                      int num_reqs);
+
 /* ------------------------------------------------------- measurement -- */
 
 /* Streaming HBM probe (no counterpart in the reference; used to state the

@@ -25,4 +25,12 @@ Parity pins (how each oracle function is checked, see tests/test_oracle_*.py):
   token_slots/materialize   reference KATs ([8,11,0,3], overlapping write,
                             padded page stride: tests/test_cache.py:15-94)
   block-table rewrite       scheduler commit semantics (pkg/stateful.py:327-338)
+  shift_positions           reference KATs ([300,20,301] with offsets [172,0] ->
+                            [128,20,129]: tests/run_npu_kernel_smoke.py:29-36;
+                            tests/test_provider_integration.py:486-514)
+  physical_seq_lens         reference KAT ([301,21] -> [129,21],
+                            tests/test_provider_integration.py:486-514)
+  brute.slot_mapping        closed form slot = table[p // 128] * 128 + p % 128
+                            (block-table arithmetic of tri/cache.py:9-15) on
+                            hand-worked cases; the GPU kernel is checked against it
 """

@@ -107,3 +107,28 @@ def order_key(x: float) -> int:
     < +inf < +NaN, so NaN ranks above every number as torch.topk ranks it."""
     bits = int(np.array(x, dtype=np.float32).view(np.uint32))
     return (~bits & 0xFFFFFFFF) if bits & 0x80000000 else (bits | 0x80000000)
+
+
+def slot_mapping(query_start_loc, positions, request_offsets, block_table, block_size, num_tokens):
+    """Slot of every token written at its physical position, by plain loops:
+    request r owns tokens [qsl[r], qsl[r+1]); p = position - offset[r];
+    slot = table[r][p // bs] * bs + p % bs, or -1 when p < 0, the block index
+    is past the table row or the entry is negative; tokens after the last
+    request are padding (-1).  Returns (slots, physical positions)."""
+    slots = [-1] * num_tokens
+    phys = [int(x) for x in positions[:num_tokens]]
+    num_reqs = len(query_start_loc) - 1
+    for r in range(num_reqs):
+        off = 0 if request_offsets is None else int(request_offsets[r])
+        for i in range(int(query_start_loc[r]), min(int(query_start_loc[r + 1]), num_tokens)):
+            p = int(positions[i]) - off
+            phys[i] = p
+            if p < 0:
+                continue
+            blk = p // block_size
+            if blk >= len(block_table[r]):
+                continue
+            page = int(block_table[r][blk])
+            if page >= 0:
+                slots[i] = page * block_size + p % block_size
+    return slots, phys

@@ -347,3 +347,18 @@ def rewrite_block_table(source_ids: list[int], destination_ids: list[int] | None
     if destination_ids is None:
         return list(source_ids[:nb]), list(reversed(source_ids[nb:]))
     return list(destination_ids[:nb]), list(reversed(source_ids))
+
+
+# ------------------------------------------------- decode after compaction --
+
+
+def shift_positions(positions: torch.Tensor, request_indices: torch.Tensor, request_offsets: torch.Tensor) -> torch.Tensor:
+    """tri/kernels.py:35-47: positions - request_offsets[request_indices]."""
+    return torch.sub(positions, request_offsets.index_select(0, request_indices.to(torch.long)))
+
+
+def physical_seq_lens(seq_lens: torch.Tensor, request_offsets: torch.Tensor, num_reqs: int) -> torch.Tensor:
+    """pkg/provider.py:707-728 (device half): seq_lens[:num_reqs] - offsets[:num_reqs]."""
+    out = seq_lens.clone()
+    out[:num_reqs].sub_(request_offsets[:num_reqs].to(out.dtype))
+    return out

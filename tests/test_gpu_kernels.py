@@ -353,3 +353,77 @@ def test_token_slots_and_expand(hip_device) -> None:
     ids = torch.tensor([3, 1], device=hip_device)
     assert cache.expand_scheduler_block_ids(ids, 16).cpu().tolist() == [48 + j for j in range(16)] + [16 + j for j in range(16)]
     assert cache.expand_scheduler_block_ids(ids, 1).cpu().tolist() == [3, 1]
+
+
+# ------------------------------------------------- decode after compaction --
+
+
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
+def test_shift_positions_matches_oracle(hip_device, index_dtype) -> None:
+    kernels, _, _ = _kvc()
+    # Reference smoke case (tests/run_npu_kernel_smoke.py:29-36).
+    pos = torch.tensor([300, 20, 301], dtype=torch.int64)
+    idx = torch.tensor([0, 1, 0], dtype=index_dtype)
+    off = torch.tensor([172, 0], dtype=torch.int64)
+    out = torch.empty(3, dtype=torch.int64, device=hip_device)
+    kernels.shift_positions(pos.to(hip_device), idx.to(hip_device), off.to(hip_device), out)
+    assert out.cpu().tolist() == [128, 20, 129]
+    # A batch of 256 requests, one decode token each plus chunked prefills.
+    g = torch.Generator().manual_seed(11)
+    n_req = 256
+    off = torch.randint(0, 30000, (n_req,), generator=g, dtype=torch.int64)
+    idx = torch.randint(0, n_req, (5000,), generator=g).to(index_dtype)
+    pos = off[idx.long()] + torch.randint(0, 4096, (5000,), generator=g, dtype=torch.int64)
+    out = torch.empty(5000, dtype=torch.int64, device=hip_device)
+    kernels.shift_positions(pos.to(hip_device), idx.to(hip_device), off.to(hip_device), out)
+    assert torch.equal(out.cpu(), ref.shift_positions(pos, idx, off))
+
+
+@pytest.mark.parametrize("with_offsets", [True, False])
+def test_physical_slot_mapping_matches_brute_force(hip_device, with_offsets: bool) -> None:
+    kernels, _, _ = _kvc()
+    g = torch.Generator().manual_seed(12)
+    n_req, max_blocks, bs = 64, 48, 128
+    q_lens = torch.randint(0, 40, (n_req,), generator=g)
+    q_lens[::3] = 1  # decode rows
+    qsl = torch.zeros(n_req + 1, dtype=torch.int32)
+    qsl[1:] = torch.cumsum(q_lens, 0).to(torch.int32)
+    n_real = int(qsl[-1])
+    num_tokens = n_real + 9  # graph padding after the last request
+    table = torch.randint(0, 5000, (n_req, max_blocks), generator=g, dtype=torch.int32)
+    table[:, 40:] = -1
+    offsets = torch.randint(0, 3000, (n_req,), generator=g, dtype=torch.int64) if with_offsets else None
+    positions = torch.empty(num_tokens, dtype=torch.int64)
+    for r in range(n_req):
+        start = int(torch.randint(0, 6000, (1,), generator=g))
+        base = (int(offsets[r]) if offsets is not None else 0) + start
+        positions[int(qsl[r]) : int(qsl[r + 1])] = torch.arange(base, base + int(q_lens[r]))
+    positions[n_real:] = torch.arange(9)
+    positions[0] = -5 if not with_offsets else positions[0]  # below zero -> -1
+    slots = torch.empty(num_tokens, dtype=torch.int64, device=hip_device)
+    phys = torch.empty(num_tokens, dtype=torch.int64, device=hip_device)
+    kernels.compute_physical_slot_mapping(
+        qsl.to(hip_device),
+        positions.to(hip_device),
+        None if offsets is None else offsets.to(hip_device),
+        table.to(hip_device),
+        bs,
+        slots,
+        phys,
+    )
+    want_slots, want_phys = brute.slot_mapping(
+        qsl.tolist(), positions.tolist(), None if offsets is None else offsets.tolist(), table.tolist(), bs, num_tokens
+    )
+    assert slots.cpu().tolist() == want_slots
+    assert phys.cpu().tolist() == want_phys
+    assert -1 in want_slots  # padding and out-of-table cases were exercised
+
+
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_shift_seq_lens_matches_oracle(hip_device, dtype) -> None:
+    kernels, _, _ = _kvc()
+    lens = torch.tensor([301, 21, 50], dtype=dtype)
+    off = torch.tensor([172, 0, 7], dtype=torch.int64)
+    dev_lens = lens.to(hip_device)
+    kernels.shift_seq_lens(dev_lens, off.to(hip_device), 2)
+    assert dev_lens.cpu().tolist() == ref.physical_seq_lens(lens, off, 2).tolist() == [129, 21, 50]

@@ -65,6 +65,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_token_slots": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p]),
     "kvc_expand_block_ids": (_i32, [_p, _p, _i64, _i32, _p]),
     "kvc_materialize_slots": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _i64, _p, _p]),
+    "kvc_shift_positions": (_i32, [_p, _p, _p, _i32, _p, _i64, _p]),
+    "kvc_physical_slot_mapping": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i64, _p, _p]),
+    "kvc_shift_lengths": (_i32, [_p, _p, _i32, _p, _i32]),
     "kvc_bandwidth_probe": (_i32, [_p, _i32, _i32, _p, _p, _i64, _i32]),
 }
 

@@ -302,3 +302,123 @@ def aggregate_normalized_scores(
         dev.ptr(aggregate),
     )
     return True
+
+
+# ------------------------------------------------------- decode after compaction --
+
+
+def shift_positions(
+    positions: torch.Tensor,
+    request_indices: torch.Tensor,
+    request_offsets: torch.Tensor,
+    output: torch.Tensor,
+) -> torch.Tensor:
+    """Physical positions of a step's tokens (tri/kernels.py:35-47):
+    ``output = positions - request_offsets[request_indices]``.
+
+    positions, request_offsets and output are int64; request_indices int32 or
+    int64 (the reference converts them to int64 before indexing)."""
+    for name, t in (("positions", positions), ("request_indices", request_indices),
+                    ("request_offsets", request_offsets), ("output", output)):
+        dev.require_hip(t, name)
+        dev.require_contiguous(t, name)
+    for name, t in (("positions", positions), ("request_offsets", request_offsets), ("output", output)):
+        dev.require_dtype(t, name, torch.int64)
+    if request_indices.dtype not in (torch.int32, torch.int64):
+        raise ValueError("request_indices must be int32 or int64")
+    n = int(positions.numel())
+    if int(request_indices.numel()) != n or int(output.numel()) != n:
+        raise ValueError("positions, request_indices and output must have the same length")
+    _native.call(
+        "kvc_shift_positions",
+        dev.stream_handle(positions.device),
+        dev.ptr(positions),
+        dev.ptr(request_indices),
+        request_indices.element_size(),
+        dev.ptr(request_offsets),
+        n,
+        dev.ptr(output),
+    )
+    return output
+
+
+def compute_physical_slot_mapping(
+    query_start_loc: torch.Tensor,
+    positions: torch.Tensor,
+    request_offsets: torch.Tensor | None,
+    block_table: torch.Tensor,
+    block_size: int,
+    slot_mapping: torch.Tensor,
+    physical_positions: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Slot mapping of a step's tokens written at their physical positions:
+    the slot-mapping hook of the reference (pkg/plugin.py:487-506 ->
+    pkg/provider.py:687-705) and the host's compute_slot_mapping in one launch.
+
+    query_start_loc: int32 [num_reqs + 1]; positions, slot_mapping (and
+    physical_positions): int64 [num_tokens]; block_table: int32
+    [>= num_reqs, max_blocks] with unit inner stride.  Padding tokens and
+    positions outside the table map to -1."""
+    for name, t in (("query_start_loc", query_start_loc), ("positions", positions),
+                    ("block_table", block_table), ("slot_mapping", slot_mapping)):
+        dev.require_hip(t, name)
+    dev.require_dtype(query_start_loc, "query_start_loc", torch.int32)
+    dev.require_dtype(positions, "positions", torch.int64)
+    dev.require_dtype(block_table, "block_table", torch.int32)
+    dev.require_dtype(slot_mapping, "slot_mapping", torch.int64)
+    if block_table.ndim != 2 or block_table.stride(1) != 1:
+        raise ValueError("block_table must be [num_reqs, max_blocks] with contiguous rows")
+    num_reqs = int(query_start_loc.numel()) - 1
+    if num_reqs < 0 or int(block_table.shape[0]) < num_reqs:
+        raise ValueError("block_table must have a row for every request")
+    num_tokens = int(positions.numel())
+    if int(slot_mapping.numel()) != num_tokens:
+        raise ValueError("slot_mapping must have one entry per token")
+    if request_offsets is not None:
+        dev.require_hip(request_offsets, "request_offsets")
+        dev.require_dtype(request_offsets, "request_offsets", torch.int64)
+        if int(request_offsets.numel()) < num_reqs:
+            raise ValueError("request_offsets must have an entry for every request")
+    if physical_positions is not None:
+        dev.require_hip(physical_positions, "physical_positions")
+        dev.require_dtype(physical_positions, "physical_positions", torch.int64)
+        if int(physical_positions.numel()) != num_tokens:
+            raise ValueError("physical_positions must have one entry per token")
+    _native.call(
+        "kvc_physical_slot_mapping",
+        dev.stream_handle(positions.device),
+        num_reqs,
+        dev.ptr(query_start_loc),
+        dev.ptr(positions),
+        dev.ptr(request_offsets),
+        dev.ptr(block_table),
+        int(block_table.stride(0)),
+        int(block_table.shape[1]),
+        int(block_size),
+        num_tokens,
+        dev.ptr(slot_mapping),
+        dev.ptr(physical_positions),
+    )
+    return slot_mapping
+
+
+def shift_seq_lens(seq_lens: torch.Tensor, request_offsets: torch.Tensor, num_reqs: int) -> torch.Tensor:
+    """``seq_lens[:num_reqs] -= request_offsets[:num_reqs]`` in place, the
+    device half of apply_physical_attention_lengths (pkg/provider.py:707-728)."""
+    dev.require_hip(seq_lens, "seq_lens")
+    dev.require_hip(request_offsets, "request_offsets")
+    dev.require_contiguous(seq_lens, "seq_lens")
+    dev.require_dtype(request_offsets, "request_offsets", torch.int64)
+    if seq_lens.dtype not in (torch.int32, torch.int64):
+        raise ValueError("seq_lens must be int32 or int64")
+    if num_reqs > int(seq_lens.numel()) or num_reqs > int(request_offsets.numel()):
+        raise ValueError("num_reqs exceeds the length or offset buffers")
+    _native.call(
+        "kvc_shift_lengths",
+        dev.stream_handle(seq_lens.device),
+        dev.ptr(seq_lens),
+        seq_lens.element_size(),
+        dev.ptr(request_offsets),
+        int(num_reqs),
+    )
+    return seq_lens
