@@ -60,14 +60,15 @@ def _run_and_check(spec, hip_device, *, check_layers=None):
     h_q = spec.num_attention_heads
     near_ties = 0
     oracle_keeps = []
+    head_mean, head_var = pipeline.head_statistics(batch)
     for b, n in enumerate(spec.seq_lens):
         out = _oracle_for(host, spec, b)
         for s_idx in range(len(spec.scoring_layers)):
             got_raw = pipeline.raw_scores()[s_idx, offs[b] : offs[b + 1], :h_q].t()
             assert_scores_close(got_raw, out["raw"][s_idx].reshape(h_q, n))
             var, mean = out["stats"][s_idx]
-            torch.testing.assert_close(pipeline.mean[s_idx, b].cpu(), mean.reshape(-1), rtol=1e-4, atol=1e-4)
-            torch.testing.assert_close(pipeline.var[s_idx, b].cpu(), var.reshape(-1), rtol=1e-3, atol=1e-4)
+            torch.testing.assert_close(head_mean[s_idx, b].cpu(), mean.reshape(-1), rtol=1e-4, atol=1e-4)
+            torch.testing.assert_close(head_var[s_idx, b].cpu(), var.reshape(-1), rtol=1e-3, atol=1e-4)
         assert_agg_close(pipeline.agg[offs[b] : offs[b + 1]], out["agg"])
         near_ties += assert_keep_matches(keep[b], out["keep"], out["agg"], spec.budget, _protected(n, spec))
         oracle_keeps.append(out["keep"])
@@ -199,3 +200,29 @@ def test_method_api_compress(hip_device, tmp_path) -> None:
     dslots = ref.token_slots(dst, torch.arange(2048, device=hip_device), 128)
     for i in range(spec.n_layers):
         assert torch.equal(cache.k_caches[i].view(-1, 8, 128)[dslots].cpu(), ref.gather_slots(host.k_caches[i], slots))
+
+
+def test_pipeline_reused_with_a_smaller_batch(hip_device) -> None:
+    """A pipeline grown by a two-sequence batch then scores one sequence: the
+    head statistics of every scoring layer must come from that call (a stale
+    stride once made layer 1 read the previous batch's sequence 0)."""
+    from kvcompress_mi355x import workloads
+    from kvcompress_mi355x.methods.triattention.pipeline import Batch
+
+    spec = workloads.config_spec(2, n_layers=4, score_layer_stride=2, seq_lens=(3000, 5000), budget=2048, recent=128, max_model_len=16384)
+    host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
+    cache = workloads.move_cache(host, hip_device)
+    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline.select_step(batch)
+    for b in (1, 0):
+        n = spec.seq_lens[b]
+        one = Batch.build(pipeline.device, [n], [n], [cache.source_tables[b]])
+        keep = pipeline.select_step(one)[0]
+        out = _oracle_for(host, spec, b)
+        assert_agg_close(pipeline.agg[:n], out["agg"])
+        mean, var = pipeline.head_statistics(one)
+        for s_idx in range(len(spec.scoring_layers)):
+            want_var, want_mean = out["stats"][s_idx]
+            torch.testing.assert_close(mean[s_idx, 0].cpu(), want_mean.reshape(-1), rtol=1e-4, atol=1e-4)
+            torch.testing.assert_close(var[s_idx, 0].cpu(), want_var.reshape(-1), rtol=1e-3, atol=1e-4)
+        assert_keep_matches(keep, out["keep"], out["agg"], spec.budget, _protected(n, spec))

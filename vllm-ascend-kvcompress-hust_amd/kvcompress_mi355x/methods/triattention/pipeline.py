@@ -261,6 +261,14 @@ class CompressionPipeline:
             return int(self.raw.stride(0)), 1, int(self.raw.stride(1))
         return int(self.raw.stride(0)), int(self.raw.stride(1)), 1
 
+    def head_statistics(self, batch: Batch) -> tuple[torch.Tensor, torch.Tensor]:
+        """Per-head mean and population variance of the last scored batch as
+        [S, batch.n_seq, H_q] views (kvc_head_stats writes them densely for the
+        batch, whatever the capacity of the buffers)."""
+        shape = (self.tables.n_layers, batch.n_seq, self.n_heads)
+        count = shape[0] * shape[1] * shape[2]
+        return self.mean.view(-1)[:count].view(shape), self.var.view(-1)[:count].view(shape)
+
     def raw_scores(self) -> torch.Tensor:
         """Raw scores as a [S, tokens, H_q] view, whatever the buffer layout."""
         return self.raw.transpose(1, 2) if self.head_major else self.raw
@@ -371,8 +379,10 @@ class CompressionPipeline:
             *self.raw_strides(),
             dev.ptr(self.mean),
             dev.ptr(self.var),
-            int(self.mean.stride(0)),
-            int(self.mean.stride(1)),
+            # kvc_head_stats wrote [S][batch.n_seq][H_q] densely; the buffer
+            # itself is sized for the pipeline's capacity.
+            batch.n_seq * self.n_heads,
+            self.n_heads,
             _native.LAYER_MEAN if self.layer_aggregation == "mean" else _native.LAYER_MAX,
             _native.AGG_FINALIZE,
             dev.ptr(self.agg),
