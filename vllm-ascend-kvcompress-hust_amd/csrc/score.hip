@@ -247,11 +247,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_paged_kernel(ScoreArgs a)
       const int k = k0 + u;
       const int t = t0 + tslot + k * tpi;
       // Unconditional loads from a row inside the pool (see the matrix-core
-      // scorer); lanes without a token or unit read offset 0 and are zeroed.
+      // scorer): iterations the prefetch reaches past the span re-read the
+      // last iteration's rows (cache hits), lanes without a unit read offset 0,
+      // and both are zeroed.
       const bool live = k < iters && t < t1 && active;
+      const int t_read = t0 + tslot + (k < iters ? k : iters - 1) * tpi;
       bool page_ok = false;
-      KVC_GLOBAL const uint16_t* pbase = pages.page(live ? t - t0 : 0, &page_ok);
-      KVC_GLOBAL const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + head_off;
+      KVC_GLOBAL const uint16_t* pbase = pages.page(t_read < t1 ? t_read - t0 : 0, &page_ok);
+      KVC_GLOBAL const uint16_t* row = pbase + static_cast<int64_t>(t_read & (kBlockSize - 1)) * row_elems + head_off;
       const w128 va = *reinterpret_cast<KVC_GLOBAL const w128*>(row + (active ? d1 : 0));
       const w128 vb = *reinterpret_cast<KVC_GLOBAL const w128*>(row + (active ? d2 : 0));
       const bool ok = live && page_ok;

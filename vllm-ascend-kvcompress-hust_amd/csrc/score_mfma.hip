@@ -213,14 +213,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
   pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0);
 
   auto load_tile = [&](int mt, u32x4 (&ka)[NK]) {
-    const int rel = mt * 16 + r;
+    // The loads are unconditional (loads under a branch would make the
+    // compiler wait for every load in flight at the join) and always hit a row
+    // inside the pool: tiles the prefetch reaches past the span re-read the
+    // span's last tile, which this wave has just read (a cache hit, not HBM
+    // traffic), and unresolved pages read page 0.  Out-of-range rows are zeroed.
+    const int mt_read = mt < n_mt ? mt : n_mt - 1;
+    const int rel = mt_read * 16 + r;
     const int t = t0 + rel;
     bool page_ok = false;
-    KVC_GLOBAL const uint16_t* pbase = pages.page(rel < kScoreTile ? rel : 0, &page_ok);
+    KVC_GLOBAL const uint16_t* pbase = pages.page(rel, &page_ok);
     const bool ok = mt < n_mt && t < t1 && page_ok;
-    // Always a row inside the pool (unresolved pages read page 0), so the loads
-    // are unconditional and rows out of range are zeroed afterwards: loads under
-    // a branch would make the compiler wait for every load in flight at the join.
     KVC_GLOBAL const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
