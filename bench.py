@@ -62,7 +62,8 @@ def parse_args() -> argparse.Namespace:
 def probe_bandwidth() -> int:
     """Achievable HBM ceilings: kvc_bandwidth_probe read / write / copy of
     4 GiB in 16-byte words, with and without non-temporal hints, over a range
-    of grid sizes; reports the best rate of each kind in GB/s."""
+    of grid sizes, and the block-contiguous pipelined copy; reports the best
+    rate of each kind in GB/s."""
     import torch
 
     from kvcompress_mi355x import _native
@@ -75,9 +76,9 @@ def probe_bandwidth() -> int:
     stream = torch.cuda.current_stream().cuda_stream
     best: dict[str, float] = {}
     detail: dict[str, float] = {}
-    for kind, name, passes in ((0, "read", 1), (1, "write", 1), (2, "copy", 2)):
-        for nt in (0, 1):
-            for blocks in (2048, 8192, 32768):
+    for kind, name, passes in ((0, "read", 1), (1, "write", 1), (2, "copy", 2), (3, "copy_chunked", 2)):
+        for nt in ((0, 1) if kind < 3 else (1,)):
+            for blocks in ((2048, 8192, 32768) if kind < 3 else (4096, 16384)):
                 for _ in range(2):
                     _native.check(lib.kvc_bandwidth_probe(stream, kind, nt, src.data_ptr(), dst.data_ptr(), size, blocks), "probe")
                 start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -260,7 +260,10 @@ int kvc_shift_lengths(kvc_stream_t stream, void* seq_lens, int elem_bytes, const
  * achievable ceilings beside the roofline): kind 0 = read `bytes` from src
  * (dst receives at most one word), 1 = write `bytes` to dst, 2 = copy src ->
  * dst; 16-byte words, grid-stride over `blocks` workgroups of 256 threads,
- * optionally with non-temporal hints.  bytes must be a multiple of 16. */
+ * optionally with non-temporal hints.  Kind 3 = copy in `blocks` contiguous
+ * chunks of 512-thread workgroups, the next 8 words per thread loaded before
+ * the current ones are stored, non-temporal (`nontemporal` ignored).  bytes
+ * must be a multiple of 16. */
 int kvc_bandwidth_probe(kvc_stream_t stream, int kind, int nontemporal, const void* src, void* dst,
                         int64_t bytes, int blocks);
 

@@ -1,6 +1,7 @@
 // HBM bandwidth probes used to state the achievable ceilings next to the
 // roofline figures: streaming read, write and copy of 16-byte words with a
-// grid-stride loop, optionally with non-temporal hints.
+// grid-stride loop, optionally with non-temporal hints (kinds 0-2), and a
+// block-contiguous, software-pipelined copy (kind 3).
 
 #include "kvc_common.h"
 
@@ -61,6 +62,44 @@ __global__ __launch_bounds__(256) void probe_copy(const w128* __restrict__ src, 
   }
 }
 
+// Block-contiguous copy: workgroup g copies words [g*per_wg, (g+1)*per_wg) in
+// steps of 8 words per thread, loading the next step before storing the
+// current one (512-thread workgroups).
+constexpr int kChunkThreads = 512;
+constexpr int kChunkUnroll = 8;
+
+__global__ __launch_bounds__(kChunkThreads) void probe_copy_chunked(const w128* __restrict__ src,
+                                                                    w128* __restrict__ dst, int64_t n,
+                                                                    int64_t per_wg) {
+  const int64_t begin = static_cast<int64_t>(blockIdx.x) * per_wg;
+  const int64_t end = begin + per_wg < n ? begin + per_wg : n;
+  const int64_t step = static_cast<int64_t>(kChunkUnroll) * kChunkThreads;
+  w128 a[kChunkUnroll], b[kChunkUnroll];
+  auto load = [&](int64_t base, w128 (&v)[kChunkUnroll]) {
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u) {
+      const int64_t j = base + u * kChunkThreads + threadIdx.x;
+      if (j < end) v[u] = __builtin_nontemporal_load(src + j);
+    }
+  };
+  auto store = [&](int64_t base, const w128 (&v)[kChunkUnroll]) {
+#pragma unroll
+    for (int u = 0; u < kChunkUnroll; ++u) {
+      const int64_t j = base + u * kChunkThreads + threadIdx.x;
+      if (j < end) __builtin_nontemporal_store(v[u], dst + j);
+    }
+  };
+  int64_t base = begin;
+  load(base, a);
+  for (; base < end; base += 2 * step) {
+    load(base + step, b);
+    store(base, a);
+    if (base + step >= end) break;
+    load(base + 2 * step, a);
+    store(base + step, b);
+  }
+}
+
 }  // namespace
 }  // namespace kvc
 
@@ -68,7 +107,7 @@ using namespace kvc;
 
 extern "C" int kvc_bandwidth_probe(kvc_stream_t stream, int kind, int nontemporal, const void* src, void* dst,
                                    int64_t bytes, int blocks) {
-  if (bytes <= 0 || bytes % 16 != 0 || blocks <= 0 || kind < 0 || kind > 2)
+  if (bytes <= 0 || bytes % 16 != 0 || blocks <= 0 || kind < 0 || kind > 3)
     return fail(KVC_EINVAL, "kvc_bandwidth_probe: bad arguments");
   if ((kind != 1 && !src) || !dst) return fail(KVC_EINVAL, "kvc_bandwidth_probe: null pointer");
   const int64_t n = bytes / 16;
@@ -81,9 +120,11 @@ extern "C" int kvc_bandwidth_probe(kvc_stream_t stream, int kind, int nontempora
   } else if (kind == 1) {
     if (nontemporal) probe_write<1><<<blocks, 256, 0, st>>>(d, n);
     else probe_write<0><<<blocks, 256, 0, st>>>(d, n);
-  } else {
+  } else if (kind == 2) {
     if (nontemporal) probe_copy<1><<<blocks, 256, 0, st>>>(s, d, n);
     else probe_copy<0><<<blocks, 256, 0, st>>>(s, d, n);
+  } else {
+    probe_copy_chunked<<<blocks, kChunkThreads, 0, st>>>(s, d, n, ceil_div(n, blocks));
   }
   return launch_status("kvc_bandwidth_probe");
 }
