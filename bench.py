@@ -56,6 +56,13 @@ def parse_args() -> argparse.Namespace:
         action="store_true",
         help="only measure streaming read / write / copy ceilings of this GPU (4 GiB buffers)",
     )
+    p.add_argument(
+        "--placement-sweep",
+        type=int,
+        default=0,
+        help="only re-allocate the workload's KV pool as one arena this many times (freeing it in between) "
+        "and report compaction time and streaming rates inside each allocation",
+    )
     return p.parse_args()
 
 
@@ -91,6 +98,81 @@ def probe_bandwidth() -> int:
                 detail[f"{name}_nt{nt}_blocks{blocks}"] = round(gbs, 1)
                 best[name] = max(best.get(name, 0.0), round(gbs, 1))
     print(json.dumps({"hbm_ceiling_gbs": best, "peak_gbs": HBM_PEAK_GBS, "detail": detail}), flush=True)
+    return 0
+
+
+def _stream_rates(lib, buf) -> dict[str, float]:
+    """Streaming read / write / block-contiguous copy (non-temporal, 8 GiB or
+    less) between the first and the second half of a device buffer, in GB/s."""
+    import torch
+
+    from kvcompress_mi355x import _native
+
+    raw = buf.view(-1).view(torch.uint8)
+    half = (raw.numel() // 2) // (1 << 30) * (1 << 30)
+    size = min(8 << 30, half)
+    if size <= 0:
+        raise ValueError("buffer too small for the streaming probe")
+    src, dst = raw[:size], raw[half : half + size]
+    stream = torch.cuda.current_stream().cuda_stream
+    rates = {}
+    for kind, name, passes, blocks in ((0, "read", 1, 32768), (1, "write", 1, 32768), (3, "copy", 2, 16384)):
+        _native.check(lib.kvc_bandwidth_probe(stream, kind, 1, src.data_ptr(), dst.data_ptr(), size, blocks), "probe")
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(3):
+            lib.kvc_bandwidth_probe(stream, kind, 1, src.data_ptr(), dst.data_ptr(), size, blocks)
+        end.record()
+        torch.cuda.synchronize()
+        rates[name] = round(passes * size / (start.elapsed_time(end) / 3) / 1e6, 1)
+    return rates
+
+
+def placement_sweep(config: int, times: int) -> int:
+    """The same KV pool placed `times` times in fresh device memory: each pass
+    allocates one arena, copies the workload's K/V pages into it, times
+    kvc_compact on it and the streaming rates inside it, and frees it."""
+    import dataclasses
+    import gc
+
+    import torch
+
+    from kvcompress_mi355x import _native, workloads
+
+    lib = _native.load()
+    spec = workloads.config_spec(config)
+    device = torch.device("cuda:0")
+    ref = workloads.build_synthetic_cache(spec, device, seed=0)
+    shape = tuple(ref.k_caches[0].shape)
+    n_pages = shape[0]
+    for i in range(times):
+        pool = torch.empty((2 * spec.n_layers * n_pages,) + shape[1:], dtype=spec.dtype, device=device)
+        ks, vs = [], []
+        for layer in range(spec.n_layers):
+            k = pool[(2 * layer) * n_pages : (2 * layer + 1) * n_pages]
+            v = pool[(2 * layer + 1) * n_pages : (2 * layer + 2) * n_pages]
+            k.copy_(ref.k_caches[layer])
+            v.copy_(ref.v_caches[layer])
+            ks.append(k)
+            vs.append(v)
+        cache = dataclasses.replace(ref, k_caches=ks, v_caches=vs)
+        pipeline, batch = workloads.build_pipeline(cache)
+        pipeline.step(batch)
+        for _ in range(3):
+            pipeline.compact(batch)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(10):
+            pipeline.compact(batch)
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / 10
+        line = {"placement": i, "arena_gib": round(pool.numel() * 2 / 2**30, 1), "compact_ms": round(ms, 4)}
+        line.update({f"{k}_gbs": v for k, v in _stream_rates(lib, pool).items()})
+        print(json.dumps(line), flush=True)
+        del pool, ks, vs, cache, pipeline, batch
+        gc.collect()
+        torch.cuda.empty_cache()
     return 0
 
 
@@ -220,6 +302,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy_mib)
     if args.probe_bandwidth:
         return probe_bandwidth()
+    if args.placement_sweep:
+        return placement_sweep(args.config, args.placement_sweep)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1

