@@ -43,6 +43,11 @@ def parse_args() -> argparse.Namespace:
         action="store_true",
         help="carve every layer's K and V pool out of one allocation instead of one allocation each",
     )
+    p.add_argument(
+        "--graph",
+        action="store_true",
+        help="capture the step once as a HIP graph and time its replays (small batches are launch-bound)",
+    )
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument(
@@ -201,36 +206,47 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def time_stages(pipeline, batch, steps: int, warmup: int):
+def time_steps(pipeline, batch, steps: int, warmup: int, graph: bool = False) -> float:
+    """Wall time of exactly `steps` compression steps (synchronised on both
+    sides), after `warmup` untimed ones; with `graph`, the step is captured
+    once and each timed step is one replay."""
     import torch
 
+    run = pipeline.capture(batch).replay if graph else (lambda: pipeline.step(batch))
     for _ in range(warmup):
-        pipeline.step(batch)
-    torch.cuda.synchronize()
-    names = ("score", "aggregate", "select", "compact", "rewrite")
-    events = {n: [] for n in names}
+        run()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-        pipeline.validate(batch)
-        marks[0].record()
-        pipeline.score(batch)
-        marks[1].record()
-        pipeline.aggregate(batch)
-        marks[2].record()
-        pipeline.select(batch)
-        marks[3].record()
-        pipeline.compact(batch)
-        marks[4].record()
-        pipeline.rewrite(batch)
-        marks[5].record()
-        for i, n in enumerate(names):
-            events[n].append((marks[i], marks[i + 1]))
+        run()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    stage_ms = {n: statistics.mean(a.elapsed_time(b) for a, b in pairs) for n, pairs in events.items()}
-    return wall, stage_ms
+    return time.perf_counter() - t0
+
+
+def stage_times(pipeline, batch, reps: int) -> dict[str, float]:
+    """Mean device time of each stage over `reps` steps, from HIP events
+    created before the loop (outside the timed steps: creating events per step
+    costs more host time than a small step's kernels)."""
+    import torch
+
+    names = ("score", "aggregate", "select", "compact", "rewrite")
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(reps)]
+    torch.cuda.synchronize()
+    for m in marks:
+        pipeline.validate(batch)
+        m[0].record()
+        pipeline.score(batch)
+        m[1].record()
+        pipeline.aggregate(batch)
+        m[2].record()
+        pipeline.select(batch)
+        m[3].record()
+        pipeline.compact(batch)
+        m[4].record()
+        pipeline.rewrite(batch)
+        m[5].record()
+    torch.cuda.synchronize()
+    return {n: statistics.mean(m[i].elapsed_time(m[i + 1]) for m in marks) for i, n in enumerate(names)}
 
 
 def cpu_baseline(cache, spec, repeats: int) -> dict:
@@ -314,7 +330,8 @@ def main() -> int:
     pipeline, batch = workloads.build_pipeline(cache)
     torch.cuda.synchronize()
 
-    wall, stage_ms = time_stages(pipeline, batch, args.steps, args.warmup)
+    wall = time_steps(pipeline, batch, args.steps, args.warmup, graph=args.graph)
+    stage_ms = stage_times(pipeline, batch, max(1, min(args.steps, 20)))
     ms_per_step = 1000.0 * wall / args.steps
     tokens = spec.total_tokens
     value = tokens / (wall / args.steps)
@@ -354,6 +371,7 @@ def main() -> int:
             "head_dim": spec.head_dim,
             "compaction": "in-place" if spec.inplace else "private destinations",
             "kv_pool": "one arena, per-layer K/V views" if args.arena else "one allocation per layer and K/V",
+            "launch": "one HIP graph per step" if args.graph else "kernel launches per step",
         },
         "roofline": {
             "kernel": "kvc_compact",

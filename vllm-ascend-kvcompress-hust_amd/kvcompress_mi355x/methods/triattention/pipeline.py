@@ -450,3 +450,41 @@ class CompressionPipeline:
             return keep, None, None
         tables, freed = self.rewrite(batch)
         return keep, tables, freed
+
+    def capture(self, batch: Batch, *, rewrite: bool = True) -> StepGraph:
+        """Record the whole step for ``batch`` as one HIP graph.
+
+        A step is about ten kernel launches; for small batches their host cost
+        exceeds the kernels' run time, and a replay issues them as one graph
+        launch.  The graph holds every launch argument, so replays run on the
+        same batch descriptors and pipeline buffers (their contents may change
+        between replays: new keys in the same pages, new calibration values,
+        new round starts).  Capacity is grown and one eager step runs first, so
+        nothing is allocated while capturing; the step makes no allocation, no
+        synchronisation and no memset of its own.
+        """
+        self.validate(batch)
+        self.ensure_capacity(batch)
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.step(batch, rewrite=rewrite)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            outputs = self.step(batch, rewrite=rewrite)
+        return StepGraph(graph, *outputs)
+
+
+@dataclass
+class StepGraph:
+    """A captured compression step; ``replay()`` enqueues it on the current
+    stream and the outputs are the step's own buffers, rewritten in place."""
+
+    graph: torch.cuda.CUDAGraph
+    keep: torch.Tensor
+    tables: torch.Tensor | None
+    freed: list[torch.Tensor] | None
+
+    def replay(self) -> None:
+        self.graph.replay()
