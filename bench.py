@@ -29,6 +29,10 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "vllm-ascend-kvcompress-hust_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# KV pool of the default workload as a serving deployment sizes it: most of
+# the 288 GB left after a 14B model's weights, 2 GiB per layer and K/V buffer
+# (192 GiB over 48 layers), with the batch's pages scattered through it.
+SERVING_POOL_PAGES = {2: 8192}
 
 
 def parse_args() -> argparse.Namespace:
@@ -38,6 +42,14 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", type=int, default=2, help="workload configuration 1-5")
     p.add_argument("--layers", type=int, default=None, help="override the materialised layer count")
+    p.add_argument(
+        "--pool-pages",
+        type=int,
+        default=None,
+        help="pages per layer and K/V buffer of the KV pool (default: 8192 = 2 GiB per buffer for the "
+        "Qwen2.5-14B 16x16384 workload, the size a serving deployment gives its pool; 0 = only the pages "
+        "the workload names); the workload's pages are scattered through the pool at random",
+    )
     p.add_argument(
         "--arena",
         action="store_true",
@@ -324,6 +336,11 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     overrides = {} if args.layers is None else {"n_layers": args.layers}
+    pool_pages = args.pool_pages
+    if pool_pages is None:
+        pool_pages = SERVING_POOL_PAGES.get(args.config, 0)
+    if pool_pages:
+        overrides["pool_pages"] = pool_pages
     spec = workloads.config_spec(args.config, **overrides)
     device = torch.device("cuda:0")
     cache = workloads.build_synthetic_cache(spec, device, seed=0, arena=args.arena)
@@ -370,7 +387,9 @@ def main() -> int:
             "heads": f"{spec.num_attention_heads}q/{spec.num_kv_heads}kv",
             "head_dim": spec.head_dim,
             "compaction": "in-place" if spec.inplace else "private destinations",
-            "kv_pool": "one arena, per-layer K/V views" if args.arena else "one allocation per layer and K/V",
+            "kv_pool": ("one arena, per-layer K/V views" if args.arena else "one allocation per layer and K/V")
+            + f", {cache.k_caches[0].shape[0]} pages each ({cache.k_caches[0].numel() * cache.k_caches[0].element_size() / 2**30:.2f} GiB)"
+            + (", workload pages scattered through it" if spec.permute_pages else ""),
             "launch": "one HIP graph per step" if args.graph else "kernel launches per step",
         },
         "roofline": {

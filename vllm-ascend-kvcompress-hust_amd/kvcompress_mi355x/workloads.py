@@ -291,13 +291,22 @@ def build_synthetic_cache(
     g = torch.Generator(device=device).manual_seed(seed)
     shape = (num_pages, KERNEL_BLOCK_SIZE, spec.num_kv_heads, spec.head_dim)
     k_caches, v_caches = [], []
+    # A pool larger than the workload (a serving-sized pool) leaves the pages
+    # no table names unwritten; only the named pages are filled.
+    named = sorted({p for t in src_tables for p in t} | {p for t in (dst_tables or []) for p in t})
+    used = range(num_pages) if len(named) == num_pages else named
+    used_index = None if len(named) == num_pages else torch.tensor(named, dtype=torch.int64, device=device)
     outlier_rows = None
     if spec.outlier_fraction > 0:
         # Outlier tokens: the same (page, row) slots in every layer, K and V scaled.
         go = torch.Generator().manual_seed(seed + 29)
-        slots = num_pages * KERNEL_BLOCK_SIZE
+        slots = len(used) * KERNEL_BLOCK_SIZE
         count = int(round(spec.outlier_fraction * slots))
-        outlier_rows = torch.randperm(slots, generator=go)[:count].to(device)
+        outlier_rows = torch.randperm(slots, generator=go)[:count]
+        if used_index is not None:
+            pages = used_index.cpu()[outlier_rows // KERNEL_BLOCK_SIZE]
+            outlier_rows = pages * KERNEL_BLOCK_SIZE + outlier_rows % KERNEL_BLOCK_SIZE
+        outlier_rows = outlier_rows.to(device)
     cg = torch.Generator().manual_seed(seed + 7)
     pool = None
     if arena:
@@ -315,12 +324,15 @@ def build_synthetic_cache(
             scale = None
             if spec.channel_scale_sigma > 0:
                 scale = (1.0 + spec.channel_scale_sigma * torch.randn(spec.num_kv_heads, spec.head_dim, generator=cg)).to(device)
-            for start in range(0, num_pages, step):
-                stop = min(num_pages, start + step)
+            for start in range(0, len(used), step):
+                stop = min(len(used), start + step)
                 chunk = torch.randn((stop - start,) + shape[1:], generator=g, device=device, dtype=torch.float32)
                 if scale is not None:
                     chunk.mul_(scale)
-                cache[start:stop].copy_(chunk)
+                if used_index is None:
+                    cache[start:stop].copy_(chunk)
+                else:
+                    cache.index_copy_(0, used_index[start:stop], chunk.to(spec.dtype))
             if outlier_rows is not None:
                 rows = cache.view(-1, spec.num_kv_heads, spec.head_dim)
                 rows[outlier_rows] = (rows[outlier_rows].float() * spec.outlier_scale).to(spec.dtype)
