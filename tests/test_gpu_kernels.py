@@ -75,6 +75,50 @@ SCORE_CASES = [
 ]
 
 
+FP16_RANGE_CASES = [
+    # (key scale, per-query-head weight scales): fp16 keys whose |k| exceeds 65504, tiny
+    # weights, and query heads whose weights differ by 10^8 (one scale per head is needed).
+    (2.0e4, (1.0, 1.0, 1.0, 1.0, 1.0)),
+    (1.0, (1e-6, 1e-6, 1e-6, 1e-6, 1e-6)),
+    (1.0, (1e-4, 1.0, 1e4, 3e-3, 250.0)),
+    (300.0, (1e3, 1e-3, 1.0, 1.0, 1e-5)),
+]
+
+
+@pytest.mark.parametrize("case", FP16_RANGE_CASES, ids=[f"k{c[0]:g}w{min(c[1]):g}-{max(c[1]):g}" for c in FP16_RANGE_CASES])
+def test_score_paged_fp16_ranges(hip_device, case) -> None:
+    kernels, _, _ = _kvc()
+    key_scale, head_scales = case
+    kv, qpk, head_dim, tokens = 8, 5, 128, 700
+    g = torch.Generator().manual_seed(len(FP16_RANGE_CASES) + tokens)
+    stats = _random_stats(g, kv, qpk, head_dim // 2, 0, head_dim)
+    w = torch.tensor(head_scales, dtype=torch.float32).view(1, qpk, 1)
+    stats = ref.LayerStats(stats.q_mean_real, stats.q_mean_imag, stats.q_abs_mean, stats.freq_scale_sq * w.square(), stats.omega,
+                           stats.rope_style, stats.rotary_dim, stats.q_pass_mean)
+    n_blocks = -(-tokens // 128)
+    pool = n_blocks + 3
+    # Keys up to +-65000 (finite fp16) put |k| up to ~92000, past fp16's largest value.
+    cache = (torch.randn(pool, 128, kv, head_dim, generator=g) * key_scale).clamp(-65000.0, 65000.0).to(torch.float16)
+    assert torch.isfinite(cache).all()
+    blocks = torch.randperm(pool, generator=g)[:n_blocks]
+    offsets = ref.build_geometric_offsets(32768)
+    round_start = tokens + 5
+    keys = ref.gather_paged_range(cache, blocks, start=0, count=tokens, block_size=128)
+    want = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets)
+    cos, sin = kernels.mean_phase_table(
+        torch.tensor([round_start], dtype=torch.int64, device=hip_device), offsets.to(hip_device), stats.omega.view(1, -1).to(hip_device)
+    )
+    out = torch.full((kv, qpk, tokens), float("nan"), device=hip_device)
+    d = lambda t: None if t is None else t.to(hip_device)  # noqa: E731
+    assert kernels.score_paged_keys_mean_precomputed(
+        cache.to(hip_device), blocks.to(hip_device), d(stats.q_mean_real), d(stats.q_mean_imag),
+        d(torch.sqrt(stats.freq_scale_sq)),
+        d(stats.q_abs_mean - torch.sqrt(stats.q_mean_real.square() + stats.q_mean_imag.square() + 1e-8)),
+        cos.view(-1), sin.view(-1), tokens, out, 128, "half",
+    )
+    assert_scores_close(out.cpu().reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
+
+
 @pytest.mark.parametrize("case", SCORE_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5])[-4:]}t{c[6]}" for c in SCORE_CASES])
 def test_score_paged_matches_oracle(hip_device, case) -> None:
     kernels, _, _ = _kvc()

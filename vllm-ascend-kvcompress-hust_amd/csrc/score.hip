@@ -685,7 +685,7 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
   sa.raw_head_stride = raw_head_stride;
   sa.partials = partials;
 
-  if (mfma_scorer_supported(s, dtype, rope_style)) return launch_mfma_scorer(st, s, fa, sa, workspace);
+  if (mfma_scorer_supported(s, dtype, rope_style)) return launch_mfma_scorer(st, s, dtype, fa, sa, workspace);
 
   const int64_t fold_threads = static_cast<int64_t>(n_seq) * n_layers * kv_heads * s.units;
   fold_weights_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 64)), 64, 0, st>>>(fa);

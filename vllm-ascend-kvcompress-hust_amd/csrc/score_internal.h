@@ -92,12 +92,18 @@ inline size_t weights_floats(const ScoreShape& s) {
   return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.units * 3 * s.qpk * 8;
 }
 // MFMA fragments: per (sequence, layer, KV head), 2*(head_dim/32) linear and
-// 2*(F/32) |k| fragments (bf16 hi/lo), each holding the 16-byte words of the
-// 4*qpk lanes of live query heads.
-inline size_t mfma_fragment_bytes(const ScoreShape& s) {
+// 2*(F/32) |k| fragments (16-bit hi/lo), each holding the 16-byte words of the
+// 4*qpk lanes of live query heads; then one float per (sequence, layer, KV
+// head, query head): the column scale the fp16 fragments are divided by.
+inline size_t mfma_fragment_only_bytes(const ScoreShape& s) {
   if (s.head_dim % 32 != 0 || s.freq % 32 != 0) return 0;
   const size_t frags = 2 * static_cast<size_t>(s.head_dim / 32) + 2 * static_cast<size_t>(s.freq / 32);
   return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * frags * 4 * s.qpk * 16;
+}
+inline size_t mfma_fragment_bytes(const ScoreShape& s) {
+  const size_t frag = mfma_fragment_only_bytes(s);
+  if (frag == 0) return 0;
+  return frag + static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk * sizeof(float);
 }
 // The weight region holds either layout.
 inline size_t weights_bytes_aligned(const ScoreShape& s) {
@@ -144,9 +150,9 @@ struct ScoreArgs {
 };
 
 // MFMA scorer (score_mfma.hip): whether it serves this shape, and its launch
-// (weight fold into bf16 hi/lo fragments + scoring).  Returns a C-ABI code.
+// (weight fold into bf16 or fp16 hi/lo fragments + scoring).  Returns a C-ABI code.
 bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style);
-int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, const FoldArgs& fa, const ScoreArgs& sa,
+int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, const ScoreArgs& sa,
                        void* weights);
 
 }  // namespace kvc

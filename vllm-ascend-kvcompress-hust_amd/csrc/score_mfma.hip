@@ -1,4 +1,5 @@
-// TriAttention paged-K scoring on the matrix cores (v_mfma_f32_16x16x32_bf16).
+// TriAttention paged-K scoring on the matrix cores (v_mfma_f32_16x16x32_bf16 /
+// v_mfma_f32_16x16x32_f16).
 //
 // The linear part of the score is a small GEMM per KV head: a 16-token x
 // head_dim tile of bf16 keys times head_dim x 16 folded weights (query heads of
@@ -18,6 +19,14 @@
 // same lane, so |k| needs no data exchange and lands exactly in the layout of
 // the magnitude GEMM's A operand.
 //
+// fp16 caches: the keys are exact fp16 A operands and the weights enter as
+// fp16 hi/lo pairs (about 22 significant bits).  fp16's range is narrow, so
+// each query head's weights (a B column) are first scaled by a power of two
+// that brings the column's largest weight to [2^13, 2^14); the column of the
+// product is scaled back on the float32 accumulator, both steps exact.  |k| is
+// scaled by 1/4 before its fp16 split (|k| of fp16 keys can exceed 65504) and
+// the magnitude weights by 4.
+//
 // Work split: a wave owns one KV head and walks 16-token tiles of its
 // workgroup's 256-token span; a workgroup covers hpw KV heads (hpw in {1,2,4}
 // dividing kv_heads) and 4/hpw interleaved tile streams per head.  The next
@@ -36,6 +45,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -44,6 +55,37 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
+// Two floats -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
+// The 16-bit element type of a cache: A/B operand vector, the MFMA, the
+// unpacking and hi/lo packing of |k|.
+template <bool F16>
+struct MfmaElem;
+template <>
+struct MfmaElem<false> {
+  typedef bf16x8 vec;
+  static constexpr float kMagScale = 1.0f;
+  __device__ __forceinline__ static f32x4 mfma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return bf16_lo(w); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return bf16_hi(w); }
+  __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_bf16(a, b); }
+};
+template <>
+struct MfmaElem<true> {
+  typedef f16x8 vec;
+  static constexpr float kMagScale = 0.25f;  // |k| of fp16 keys reaches 2^16.5
+  __device__ __forceinline__ static f32x4 mfma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return fp16_lo(w); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return fp16_hi(w); }
+  __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_f16(a, b); }
+};
 
 // K is read once per scoring layer.  Non-temporal loads (meant to keep K from
 // evicting the weight fragments in L2) measured 0.85 ms against 0.72 ms for
@@ -96,6 +138,30 @@ inline MfmaGeometry geometry(const ScoreShape& s) {
 // Magnitude weight of frequency f: sqrt(fss) * extra.  Fragments 2j / 2j+1
 // hold the hi / lo bf16 parts of linear step j, 2nk+2q / 2nk+2q+1 those of
 // magnitude step q.
+// Folded weight of K-step element (step, kb, e) for query head g of
+// (sequence b, layer, KV head): see fold_mfma_kernel.
+__device__ __forceinline__ float folded_weight(const FoldArgs& a, int nk, int b, int layer, int64_t row, int step,
+                                              int kb, int e) {
+  const int head_dim = a.rotary_dim + a.pass;
+  if (step < nk) {
+    const int d = 32 * step + 8 * kb + e;
+    if (d >= head_dim) return 0.0f;
+    if (d < 2 * a.freq) {
+      const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
+      const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
+      const int f = d < a.freq ? d : d - a.freq;
+      const int64_t o = row * a.freq + f;
+      const float qr = a.q_real[o], qi = a.q_imag[o], sc = a.scale[o];
+      const float c = pc[f], sn = ps[f];
+      return d < a.freq ? sc * (qr * c - qi * sn) : sc * (qi * c + qr * sn);
+    }
+    return a.q_pass[row * a.pass + (d - a.rotary_dim)];
+  }
+  const int f = 32 * (step - nk) + 8 * kb + e;
+  const int64_t o = row * a.freq + f;
+  return a.scale[o] * a.extra[o];
+}
+
 __global__ void fold_mfma_kernel(FoldArgs a, int nk, int nf, uint16_t* __restrict__ frags) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int n_frag = 2 * nk + 2 * nf;
@@ -113,33 +179,12 @@ __global__ void fold_mfma_kernel(FoldArgs a, int nk, int nf, uint16_t* __restric
   const int g = pl % a.qpk;
   const int kb = pl / a.qpk;
   const int64_t row = ((static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + g);
-  const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
-  const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
-  const int head_dim = a.rotary_dim + a.pass;
   const bool low = (frag & 1) != 0;
   const int step = frag >> 1;
   uint16_t out[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float w = 0.0f;
-    if (step < nk) {
-      const int d = 32 * step + 8 * kb + e;
-      if (d < head_dim) {
-        if (d < 2 * a.freq) {
-          const int f = d < a.freq ? d : d - a.freq;
-          const int64_t o = row * a.freq + f;
-          const float qr = a.q_real[o], qi = a.q_imag[o], sc = a.scale[o];
-          const float c = pc[f], sn = ps[f];
-          w = d < a.freq ? sc * (qr * c - qi * sn) : sc * (qi * c + qr * sn);
-        } else {
-          w = a.q_pass[row * a.pass + (d - a.rotary_dim)];
-        }
-      }
-    } else {
-      const int f = 32 * (step - nk) + 8 * kb + e;
-      const int64_t o = row * a.freq + f;
-      w = a.scale[o] * a.extra[o];
-    }
+    const float w = folded_weight(a, nk, b, layer, row, step, kb, e);
     const uint32_t hi = bf16_bits(w);
     out[e] = static_cast<uint16_t>(low ? bf16_bits(w - bf16_value(hi)) : hi);
   }
@@ -148,11 +193,77 @@ __global__ void fold_mfma_kernel(FoldArgs a, int nk, int nf, uint16_t* __restric
   for (int e = 0; e < 8; ++e) dst[e] = out[e];
 }
 
+// fp16 fragments: one wave per (sequence, layer, KV head, query head g), 256
+// threads per workgroup.  Lane l < 4*(nk+nf) owns K step l/4, row block l%4:
+// its eight weights (magnitude weights times 1/kMagScale), then the column's
+// largest magnitude over the wave picks the power-of-two scale 2^s that brings
+// it to [2^13, 2^14) (s in [-126, 126]; none when it is 0, inf or NaN).  The
+// lane writes fp16(2^s w) and fp16(2^s w - hi) to fragments 2 step and
+// 2 step + 1 in the packed layout of fold_mfma_kernel; lane 0 writes 2^-s.
+__global__ __launch_bounds__(256) void fold_mfma_f16_kernel(FoldArgs a, int nk, int nf, uint16_t* __restrict__ frags,
+                                                            float* __restrict__ inv_scale) {
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t cols = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * a.qpk;
+  if (col >= cols) return;  // whole wave
+  const int lane = threadIdx.x & 63;
+  const int g = static_cast<int>(col % a.qpk);
+  int64_t r = col / a.qpk;
+  const int head = static_cast<int>(r % a.kv_heads);
+  r /= a.kv_heads;
+  const int layer = static_cast<int>(r % a.n_layers);
+  const int b = static_cast<int>(r / a.n_layers);
+  const int64_t row = ((static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + g);
+  const bool active = lane < 4 * (nk + nf);
+  const int step = lane >> 2, kb = lane & 3;
+  float w[8];
+  float big = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    w[e] = active ? folded_weight(a, nk, b, layer, row, step, kb, e) : 0.0f;
+    if (step >= nk) w[e] *= 1.0f / MfmaElem<true>::kMagScale;
+    big = fmaxf(big, fabsf(w[e]));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) big = fmaxf(big, __shfl_xor(big, off));
+  int sh = 0;
+  if (big > 0.0f && big <= 3.4e38f) {
+    int ex;
+    (void)frexpf(big, &ex);  // big < 2^ex
+    sh = 14 - ex;
+    sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+  }
+  if (active) {
+    const int n_frag = 2 * nk + 2 * nf;
+    const int packed = 4 * a.qpk;
+    const int64_t base = (((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * n_frag + 2 * step) * packed +
+                         kb * a.qpk + g;
+    uint16_t hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = ldexpf(w[e], sh);
+      const _Float16 h = static_cast<_Float16>(v);
+      hi[e] = __builtin_bit_cast(uint16_t, h);
+      lo[e] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(v - static_cast<float>(h)));
+    }
+    uint16_t* dhi = frags + base * 8;
+    uint16_t* dlo = frags + (base + packed) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      dhi[e] = hi[e];
+      dlo[e] = lo[e];
+    }
+  }
+  if (lane == 0) inv_scale[col] = ldexpf(1.0f, -sh);
+}
+
 // --------------------------------------------------------------- score ------
 
-template <int NK, int NF>
+template <int NK, int NF, bool F16>
 __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, MfmaGeometry geo, int qpk,
-                                                                   const u32x4* __restrict__ frags) {
+                                                                   const u32x4* __restrict__ frags,
+                                                                   const float* __restrict__ inv_scale) {
+  typedef MfmaElem<F16> E;
+  typedef typename E::vec vec_t;
   const int layer = blockIdx.z;
   const int b = blockIdx.y;
   const int tile = blockIdx.x / geo.head_groups;
@@ -179,9 +290,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
                     kb * qpk + (live_col ? r : 0);
   auto frag_word = [&](int f) {
     const u32x4 v = fp[f * packed];
-    return __builtin_bit_cast(bf16x8, live_col ? v : u32x4{0, 0, 0, 0});
+    return __builtin_bit_cast(vec_t, live_col ? v : u32x4{0, 0, 0, 0});
   };
-  bf16x8 w_hi[NK], w_lo[NK], m_hi[NF], m_lo[NF];
+  vec_t w_hi[NK], w_lo[NK], m_hi[NF], m_lo[NF];
+  // fp16: the scale that takes this lane's output column back from the
+  // scaled weights.
+  const float col_scale =
+      F16 ? inv_scale[((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * qpk + (live_col ? r : 0)]
+          : 1.0f;
 #pragma unroll
   for (int j = 0; j < NK; ++j) {
     w_hi[j] = frag_word(2 * j);
@@ -239,13 +355,13 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      const bf16x8 kv = __builtin_bit_cast(bf16x8, ka[j]);
+      const vec_t kv = __builtin_bit_cast(vec_t, ka[j]);
       if (j & 1) {
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_hi[j], acc1, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_lo[j], acc1, 0, 0, 0);
+        acc1 = E::mfma(kv, w_hi[j], acc1);
+        acc1 = E::mfma(kv, w_lo[j], acc1);
       } else {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_hi[j], acc0, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, w_lo[j], acc0, 0, 0, 0);
+        acc0 = E::mfma(kv, w_hi[j], acc0);
+        acc0 = E::mfma(kv, w_lo[j], acc0);
       }
     }
 #pragma unroll
@@ -254,21 +370,22 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const uint32_t re_w = ka[q][w], im_w = ka[q + NF][w];
-        const float re0 = bf16_lo(re_w), re1 = bf16_hi(re_w);
-        const float im0 = bf16_lo(im_w), im1 = bf16_hi(im_w);
-        const float m0 = __builtin_amdgcn_sqrtf(fmaf(im0, im0, re0 * re0));
-        const float m1 = __builtin_amdgcn_sqrtf(fmaf(im1, im1, re1 * re1));
-        const uint32_t h = pack_bf16(m0, m1);
+        const float re0 = E::lo(re_w), re1 = E::hi(re_w);
+        const float im0 = E::lo(im_w), im1 = E::hi(im_w);
+        const float m0 = __builtin_amdgcn_sqrtf(fmaf(im0, im0, re0 * re0)) * E::kMagScale;
+        const float m1 = __builtin_amdgcn_sqrtf(fmaf(im1, im1, re1 * re1)) * E::kMagScale;
+        const uint32_t h = E::pack(m0, m1);
         hi[w] = h;
-        lo[w] = pack_bf16(m0 - bf16_lo(h), m1 - bf16_hi(h));
+        lo[w] = E::pack(m0 - E::lo(h), m1 - E::hi(h));
       }
-      const bf16x8 khi = __builtin_bit_cast(bf16x8, hi);
-      const bf16x8 klo = __builtin_bit_cast(bf16x8, lo);
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_hi[q], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, m_lo[q], acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, m_hi[q], acc0, 0, 0, 0);
+      const vec_t khi = __builtin_bit_cast(vec_t, hi);
+      const vec_t klo = __builtin_bit_cast(vec_t, lo);
+      acc0 = E::mfma(khi, m_hi[q], acc0);
+      acc1 = E::mfma(khi, m_lo[q], acc1);
+      acc0 = E::mfma(klo, m_hi[q], acc0);
     }
-    const f32x4 acc = acc0 + acc1;
+    f32x4 acc = acc0 + acc1;
+    if (F16) acc *= col_scale;
     // D[4*kb + i][r]: token t0 + 16*mt + 4*kb + i, query head r of this KV head.
     // Scores go to the workgroup's LDS stage (four adjacent tokens per lane,
     // one 16-byte write); global stores wait until the span is done, so the
@@ -362,41 +479,51 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
   }
 }
 
-using MfmaKernel = void (*)(ScoreArgs, MfmaGeometry, int, const u32x4*);
+using MfmaKernel = void (*)(ScoreArgs, MfmaGeometry, int, const u32x4*, const float*);
 
-MfmaKernel pick(int nk, int nf) {
+template <bool F16>
+MfmaKernel pick_typed(int nk, int nf) {
   switch (nk * 16 + nf) {
-    case 2 * 16 + 1: return score_mfma_kernel<2, 1>;
-    case 4 * 16 + 1: return score_mfma_kernel<4, 1>;
-    case 4 * 16 + 2: return score_mfma_kernel<4, 2>;
-    case 8 * 16 + 1: return score_mfma_kernel<8, 1>;
-    case 8 * 16 + 2: return score_mfma_kernel<8, 2>;
-    case 8 * 16 + 4: return score_mfma_kernel<8, 4>;
+    case 2 * 16 + 1: return score_mfma_kernel<2, 1, F16>;
+    case 4 * 16 + 1: return score_mfma_kernel<4, 1, F16>;
+    case 4 * 16 + 2: return score_mfma_kernel<4, 2, F16>;
+    case 8 * 16 + 1: return score_mfma_kernel<8, 1, F16>;
+    case 8 * 16 + 2: return score_mfma_kernel<8, 2, F16>;
+    case 8 * 16 + 4: return score_mfma_kernel<8, 4, F16>;
     default: return nullptr;
   }
+}
+MfmaKernel pick(int nk, int nf, int dtype) {
+  return dtype == KVC_DTYPE_FP16 ? pick_typed<true>(nk, nf) : pick_typed<false>(nk, nf);
 }
 
 }  // namespace
 
 bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style) {
-  if (dtype != KVC_DTYPE_BF16 || rope_style != KVC_ROPE_HALF) return false;
+  if ((dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16) || rope_style != KVC_ROPE_HALF) return false;
   if (s.head_dim % 32 != 0 || s.freq % 32 != 0 || s.qpk > kMfmaMaxQpk) return false;
-  return pick(s.head_dim / 32, s.freq / 32) != nullptr;
+  return pick(s.head_dim / 32, s.freq / 32, dtype) != nullptr;
 }
 
-int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, const FoldArgs& fa, const ScoreArgs& sa,
+int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, const ScoreArgs& sa,
                        void* weights) {
   const MfmaGeometry geo = geometry(s);
-  MfmaKernel kern = pick(geo.nk, geo.nf);
+  MfmaKernel kern = pick(geo.nk, geo.nf, dtype);
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: no MFMA scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
-  const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * (2 * geo.nk + 2 * geo.nf) * 4 * s.qpk;
-  fold_mfma_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 256)), 256, 0, stream>>>(
-      fa, geo.nk, geo.nf, static_cast<uint16_t*>(weights));
+  uint16_t* frags = static_cast<uint16_t*>(weights);
+  float* inv_scale = reinterpret_cast<float*>(static_cast<char*>(weights) + mfma_fragment_only_bytes(s));
+  if (dtype == KVC_DTYPE_FP16) {
+    const int64_t cols = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
+    fold_mfma_f16_kernel<<<static_cast<unsigned>(ceil_div(cols, 4)), 256, 0, stream>>>(fa, geo.nk, geo.nf, frags, inv_scale);
+  } else {
+    const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * (2 * geo.nk + 2 * geo.nf) * 4 * s.qpk;
+    fold_mfma_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 256)), 256, 0, stream>>>(fa, geo.nk, geo.nf, frags);
+  }
   if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
   const int64_t gx = static_cast<int64_t>(s.max_tiles) * geo.head_groups;
   if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_score_paged: grid too large");
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(s.n_seq), static_cast<unsigned>(s.n_layers));
-  kern<<<grid, kScoreThreads, 0, stream>>>(sa, geo, s.qpk, static_cast<const u32x4*>(weights));
+  kern<<<grid, kScoreThreads, 0, stream>>>(sa, geo, s.qpk, reinterpret_cast<const u32x4*>(frags), inv_scale);
   return launch_status("kvc_score_paged");
 }
 

@@ -291,8 +291,8 @@ def build_synthetic_cache(
     g = torch.Generator(device=device).manual_seed(seed)
     shape = (num_pages, KERNEL_BLOCK_SIZE, spec.num_kv_heads, spec.head_dim)
     k_caches, v_caches = [], []
-    # A pool larger than the workload (a serving-sized pool) leaves the pages
-    # no table names unwritten; only the named pages are filled.
+    # A pool larger than the workload (a serving-sized pool) fills only the
+    # pages the tables name; the others hold zeros.
     named = sorted({p for t in src_tables for p in t} | {p for t in (dst_tables or []) for p in t})
     used = range(num_pages) if len(named) == num_pages else named
     used_index = None if len(named) == num_pages else torch.tensor(named, dtype=torch.int64, device=device)
@@ -310,7 +310,8 @@ def build_synthetic_cache(
     cg = torch.Generator().manual_seed(seed + 7)
     pool = None
     if arena:
-        pool = torch.empty((2 * spec.n_layers * num_pages,) + shape[1:], dtype=spec.dtype, device=device)
+        alloc = torch.empty if used_index is None else torch.zeros
+        pool = alloc((2 * spec.n_layers * num_pages,) + shape[1:], dtype=spec.dtype, device=device)
     for layer in range(spec.n_layers):
         caches = []
         for kind in range(2):
@@ -318,7 +319,7 @@ def build_synthetic_cache(
                 start = (2 * layer + kind) * num_pages
                 cache = pool[start : start + num_pages]
             else:
-                cache = torch.empty(shape, dtype=spec.dtype, device=device)
+                cache = (torch.empty if used_index is None else torch.zeros)(shape, dtype=spec.dtype, device=device)
             flat = cache.view(num_pages, -1)
             step = max(1, (1 << 26) // flat.shape[1])  # fill in bounded float32 chunks
             scale = None
