@@ -72,6 +72,13 @@ SCORE_CASES = [
     (1, 8, 256, 64, "half", torch.bfloat16, 130),
     (4, 1, 128, 128, "half", torch.bfloat16, 129),
     (16, 2, 64, 64, "half", torch.bfloat16, 300),
+    # interleaved RoPE on the matrix cores (bf16, fp16, partial rotary)
+    (8, 5, 128, 128, "interleaved", torch.bfloat16, 700),
+    (8, 5, 128, 128, "interleaved", torch.float16, 513),
+    (2, 8, 256, 64, "interleaved", torch.bfloat16, 300),
+    # VALU scorer: frequency counts that are not a multiple of 32
+    (4, 4, 128, 32, "half", torch.bfloat16, 400),
+    (2, 6, 96, 96, "interleaved", torch.float16, 350),
 ]
 
 

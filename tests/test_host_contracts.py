@@ -288,3 +288,25 @@ def test_workspace_query_and_argument_validation_without_gpu() -> None:
         _native.call("kvc_select_keep", None, 1, 10, None, None, None, 20, 0, 0, 1, 0, None, 20)
     with pytest.raises(ValueError):
         _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4)
+
+
+def test_raw_layout_names_the_scorer_without_gpu() -> None:
+    """Matrix-core shapes (bf16 or fp16, half or interleaved RoPE, head_dim and
+    F multiples of 32, qpk <= 8) get head-major raw scores; the rest token-major."""
+    from kvcompress_mi355x import _native
+
+    lib = _native.load()
+    bf16, fp16 = 0, 1
+    half, interleaved = 0, 1
+    head, token = _native.RAW_HEAD_MAJOR, _native.RAW_TOKEN_MAJOR
+    cases = [
+        ((bf16, half, 8, 128, 128, 5), head),
+        ((fp16, half, 8, 128, 128, 5), head),
+        ((bf16, interleaved, 8, 128, 128, 5), head),
+        ((fp16, interleaved, 2, 256, 64, 8), head),
+        ((bf16, half, 4, 128, 32, 4), token),  # F = 16
+        ((fp16, interleaved, 2, 96, 96, 6), token),  # F = 48
+    ]
+    for args, want in cases:
+        assert lib.kvc_score_raw_layout(*args) == want, args
+    assert lib.kvc_score_raw_layout(7, half, 8, 128, 128, 5) < 0  # unknown dtype

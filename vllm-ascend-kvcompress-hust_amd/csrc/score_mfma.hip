@@ -19,6 +19,12 @@
 // same lane, so |k| needs no data exchange and lands exactly in the layout of
 // the magnitude GEMM's A operand.
 //
+// Interleaved RoPE keeps (real, imaginary) of frequency f in dims (2f, 2f+1),
+// so each 32-bit word of a lane's K chunk is one frequency: linear steps 2q and
+// 2q+1 give the lane 4 + 4 magnitudes, frequencies 16(2q+h) + 4*(l/16) + i for
+// h in {0,1}, i < 4, which fill magnitude step q (the fold lays the magnitude
+// weights out in the same order), again without a data exchange.
+//
 // fp16 caches: the keys are exact fp16 A operands and the weights enter as
 // fp16 hi/lo pairs (about 22 significant bits).  fp16's range is narrow, so
 // each query head's weights (a B column) are first scaled by a power of two
@@ -149,15 +155,18 @@ __device__ __forceinline__ float folded_weight(const FoldArgs& a, int nk, int b,
     if (d < 2 * a.freq) {
       const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
       const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
-      const int f = d < a.freq ? d : d - a.freq;
+      // Half style: real parts in dims [0, F), imaginary in [F, 2F); interleaved: (2f, 2f+1).
+      const bool real = a.interleaved ? (d & 1) == 0 : d < a.freq;
+      const int f = a.interleaved ? d >> 1 : (d < a.freq ? d : d - a.freq);
       const int64_t o = row * a.freq + f;
       const float qr = a.q_real[o], qi = a.q_imag[o], sc = a.scale[o];
       const float c = pc[f], sn = ps[f];
-      return d < a.freq ? sc * (qr * c - qi * sn) : sc * (qi * c + qr * sn);
+      return real ? sc * (qr * c - qi * sn) : sc * (qi * c + qr * sn);
     }
     return a.q_pass[row * a.pass + (d - a.rotary_dim)];
   }
-  const int f = 32 * (step - nk) + 8 * kb + e;
+  const int q = step - nk;
+  const int f = a.interleaved ? 16 * (2 * q + (e >> 2)) + 4 * kb + (e & 3) : 32 * q + 8 * kb + e;
   const int64_t o = row * a.freq + f;
   return a.scale[o] * a.extra[o];
 }
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(256) void fold_mfma_f16_kernel(FoldArgs a, int nk, 
 
 // --------------------------------------------------------------- score ------
 
-template <int NK, int NF, bool F16>
+template <int NK, int NF, bool F16, bool IL>
 __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, MfmaGeometry geo, int qpk,
                                                                    const u32x4* __restrict__ frags,
                                                                    const float* __restrict__ inv_scale) {
@@ -369,7 +378,19 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
       u32x4 hi, lo;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t re_w = ka[q][w], im_w = ka[q + NF][w];
+        // Two frequencies per output word: half style pairs word w of steps q
+        // (real) and q+NF (imaginary); interleaved takes words 2w, 2w+1 of
+        // step 2q (w < 2) or 2q+1, each word one (real, imaginary) pair.
+        uint32_t re_w, im_w;
+        if (IL) {
+          const uint32_t w0 = ka[2 * q + (w >> 1)][(2 * w) & 3], w1 = ka[2 * q + (w >> 1)][(2 * w + 1) & 3];
+          // (re0, re1) = (lo of w0, lo of w1), (im0, im1) = (hi of w0, hi of w1)
+          re_w = (w0 & 0xffffu) | (w1 << 16);
+          im_w = (w0 >> 16) | (w1 & 0xffff0000u);
+        } else {
+          re_w = ka[q][w];
+          im_w = ka[q + NF][w];
+        }
         const float re0 = E::lo(re_w), re1 = E::hi(re_w);
         const float im0 = E::lo(im_w), im1 = E::hi(im_w);
         const float m0 = __builtin_amdgcn_sqrtf(fmaf(im0, im0, re0 * re0)) * E::kMagScale;
@@ -481,34 +502,37 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
 
 using MfmaKernel = void (*)(ScoreArgs, MfmaGeometry, int, const u32x4*, const float*);
 
-template <bool F16>
+template <bool F16, bool IL>
 MfmaKernel pick_typed(int nk, int nf) {
   switch (nk * 16 + nf) {
-    case 2 * 16 + 1: return score_mfma_kernel<2, 1, F16>;
-    case 4 * 16 + 1: return score_mfma_kernel<4, 1, F16>;
-    case 4 * 16 + 2: return score_mfma_kernel<4, 2, F16>;
-    case 8 * 16 + 1: return score_mfma_kernel<8, 1, F16>;
-    case 8 * 16 + 2: return score_mfma_kernel<8, 2, F16>;
-    case 8 * 16 + 4: return score_mfma_kernel<8, 4, F16>;
+    case 2 * 16 + 1: return score_mfma_kernel<2, 1, F16, IL>;
+    case 4 * 16 + 1: return score_mfma_kernel<4, 1, F16, IL>;
+    case 4 * 16 + 2: return score_mfma_kernel<4, 2, F16, IL>;
+    case 8 * 16 + 1: return score_mfma_kernel<8, 1, F16, IL>;
+    case 8 * 16 + 2: return score_mfma_kernel<8, 2, F16, IL>;
+    case 8 * 16 + 4: return score_mfma_kernel<8, 4, F16, IL>;
     default: return nullptr;
   }
 }
-MfmaKernel pick(int nk, int nf, int dtype) {
-  return dtype == KVC_DTYPE_FP16 ? pick_typed<true>(nk, nf) : pick_typed<false>(nk, nf);
+MfmaKernel pick(int nk, int nf, int dtype, int rope_style) {
+  const bool il = rope_style == KVC_ROPE_INTERLEAVED;
+  if (dtype == KVC_DTYPE_FP16) return il ? pick_typed<true, true>(nk, nf) : pick_typed<true, false>(nk, nf);
+  return il ? pick_typed<false, true>(nk, nf) : pick_typed<false, false>(nk, nf);
 }
 
 }  // namespace
 
 bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style) {
-  if ((dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16) || rope_style != KVC_ROPE_HALF) return false;
+  if (dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16) return false;
+  if (rope_style != KVC_ROPE_HALF && rope_style != KVC_ROPE_INTERLEAVED) return false;
   if (s.head_dim % 32 != 0 || s.freq % 32 != 0 || s.qpk > kMfmaMaxQpk) return false;
-  return pick(s.head_dim / 32, s.freq / 32, dtype) != nullptr;
+  return pick(s.head_dim / 32, s.freq / 32, dtype, rope_style) != nullptr;
 }
 
 int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, const ScoreArgs& sa,
                        void* weights) {
   const MfmaGeometry geo = geometry(s);
-  MfmaKernel kern = pick(geo.nk, geo.nf, dtype);
+  MfmaKernel kern = pick(geo.nk, geo.nf, dtype, fa.interleaved ? KVC_ROPE_INTERLEAVED : KVC_ROPE_HALF);
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: no MFMA scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
   uint16_t* frags = static_cast<uint16_t*>(weights);
   float* inv_scale = reinterpret_cast<float*>(static_cast<char*>(weights) + mfma_fragment_only_bytes(s));
