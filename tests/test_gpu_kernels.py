@@ -299,7 +299,7 @@ def _layers(g, n_layers, pages, kv, dim, dtype):
 
 
 @pytest.mark.parametrize("mode", ["private", "inplace"])
-@pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided"])
+@pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided", "split"])
 def test_compact_bit_exact(hip_device, mode: str, pattern: str) -> None:
     _, _, cache = _kvc()
     from kvcompress_mi355x.methods.triattention import _device as dev
@@ -323,8 +323,13 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str) -> None:
     for n in lens:
         if pattern == "random":
             k = torch.sort(torch.randperm(n, generator=g)[:budget]).values
-        elif pattern == "front":
+        elif pattern == "front" or (pattern == "split" and n < 2 * budget):
             k = torch.arange(budget)
+        elif pattern == "split":
+            # In place, the first half reads rows 1, 3, 5, ... below the budget,
+            # which the second half (sources at or past the budget) overwrites.
+            half = budget // 2
+            k = torch.cat([2 * torch.arange(half) + 1, torch.arange(budget, 2 * budget - half)])
         elif pattern == "tail":
             k = torch.arange(n - budget, n)
         else:

@@ -14,30 +14,40 @@
 // words of the tile together before storing them, so the index chase is paid
 // once per tile instead of once per layer.
 //
-// In-place mode (destinations are the sequence's own front pages): keep is
-// strictly increasing, so keep[j] >= j and the source row of destination j can
-// only be overwritten by a destination i >= j.  A workgroup owns one column
-// slice of one (layer, sequence) and walks the rows in ascending tiles: every
-// load of a tile (K and V) completes before a workgroup barrier, then the
-// tile's stores go out.  A row read by tile T lies at index >= the first row
-// of tile T, so it is overwritten, if at all, by tile T itself (after the
-// barrier) or by a later tile.  Column slices are disjoint bytes, so slices
-// run in parallel.  Rows whose source and destination coincide are skipped.
+// In-place mode (destinations are the sequence's own front pages, rows
+// [0, budget)): keep is strictly increasing, so keep[j] >= j, and the rows
+// split at J0, the first j with keep[j] >= budget:
+//  * hazard rows j < J0 read a row below the budget, which another
+//    destination may overwrite (row r is written by destination r >= j).  A
+//    workgroup owns one column slice of one (layer, sequence) and walks these
+//    rows in ascending tiles: every load of a tile (K and V) completes before
+//    a workgroup barrier, then the tile's stores go out.  A row read by tile T
+//    lies at index >= the first row of tile T, so it is overwritten, if at
+//    all, by tile T itself (after the barrier) or by a later tile.  The walk
+//    stops at the first tile that starts at or after J0.
+//  * safe rows j >= J0 read rows >= budget, which no destination writes, and
+//    write rows in [J0, budget), which only hazard rows read.  A second launch
+//    (the private-mode kernel over the same table) moves them with no
+//    ordering at all once the walk has finished.
+// Column slices are disjoint bytes, so slices run in parallel.  Rows whose
+// source and destination coincide are skipped.
 
 #include "kvc_common.h"
 
 namespace kvc {
 namespace {
 
-// Private mode: one row per thread and 512-thread workgroups keep the most
-// waves resident; on the Qwen2.5-14B shape (16 x 4096 kept rows, 48 layers)
-// this measured 4.13 ms against 4.36 ms for 4 rows and 4.84 ms for 8 rows
-// per thread at 256 threads.
+// Row-parallel kernel: one row per thread, 256-thread workgroups.  Timed on
+// fresh data in one allocation, against 512 threads: 4.27 vs 4.29 ms
+// (Qwen2.5-14B shape, 16 x 4096 kept rows of 2 KB, 48 layers), 1.43 vs
+// 1.50 ms (4 x 4608 rows kept of 131072, in place), 0.286 vs 0.296 ms
+// (Qwen3.5 shape, 1 KB rows); 2 or 4 rows per thread and 1024 threads were
+// slower on all three, 128 threads level with 256.
 #ifndef KVC_COPY_UNROLL
 #define KVC_COPY_UNROLL 1
 #endif
 #ifndef KVC_COPY_THREADS
-#define KVC_COPY_THREADS 512
+#define KVC_COPY_THREADS 256
 #endif
 // In-place mode walks its tiles in order behind a barrier; 2 rows per thread
 // at 512 threads measured 0.85 ms on the 4 x 131072-token shape (48 layers,
@@ -86,7 +96,12 @@ struct CompactArgs {
   const int64_t* dst_ids;
   const int64_t* keep;
   int64_t keep_stride;
+  int rows;              // kRowsAll, or the in-place halves kRowsHazard / kRowsSafe
 };
+
+constexpr int kRowsAll = 0;
+constexpr int kRowsHazard = 1;  // keep[i] < budget (in place, ordered walk)
+constexpr int kRowsSafe = 2;    // keep[i] >= budget (in place, any order)
 
 // Streaming word access; the non-temporal forms mark lines for early eviction.
 template <typename Chunk>
@@ -124,6 +139,7 @@ __device__ __forceinline__ RowMove resolve_row(const CompactArgs& a, const int64
   if (!col_ok || i >= a.budget) return m;
   const int64_t src_row = kp[i];
   if (src_row < 0 || src_row >= n_tokens) return m;
+  if (a.rows != kRowsAll && (src_row < a.budget) != (a.rows == kRowsHazard)) return m;
   const int64_t sp = page_of(sbt, n_src, src_row, a.num_pages);
   const int64_t dp = page_of(dbt, n_dst, i, a.num_pages);
   if (sp < 0 || dp < 0) return m;
@@ -154,8 +170,9 @@ __device__ __forceinline__ void resolve_tile(const CompactArgs& a, int b, int64_
   }
 }
 
-// Private mode: a workgroup moves the K and V words of one row tile x one
-// column slice of one sequence through every layer.
+// Row-parallel kernel (private mode, and the safe rows of in-place mode): a
+// workgroup moves the K and V words of one row tile x one column slice of one
+// sequence through every layer.
 template <typename Chunk>
 __global__ __launch_bounds__(kCopyThreads) void compact_private_kernel(CompactArgs a) {
   // One-dimensional grid, sequence fastest: the workgroups resident at a time
@@ -198,9 +215,17 @@ __global__ __launch_bounds__(kCopyThreads) void compact_private_kernel(CompactAr
   }
 }
 
-// Rows of tile `tile` moved in place inside one sequence's own pages.
+// Whether the walk reaches tile `tile`: the tile starts inside the budget at
+// a hazard row (keep is increasing, so no hazard row follows a safe one).
+// The same value in every thread of the workgroup.
+__device__ __forceinline__ bool hazard_tile(const CompactArgs& a, const int64_t* kp, int tile, int tile_rows) {
+  const int64_t first = static_cast<int64_t>(tile) * tile_rows;
+  return first < a.budget && kp[first] < a.budget;
+}
+
+// Hazard rows of tile `tile`, moved in place inside one sequence's own pages.
 template <int U>
-__device__ __forceinline__ void resolve_inplace(const CompactArgs& a, int b, int tile, int n_tiles, int tile_rows,
+__device__ __forceinline__ void resolve_inplace(const CompactArgs& a, int b, int tile, bool live, int tile_rows,
                                                 int rows_per_step, int row_lane, int64_t word_off, bool col_ok,
                                                 RowMove (&mv)[U]) {
   const int64_t* sbt = a.src_ids + a.src_off[b];
@@ -210,16 +235,16 @@ __device__ __forceinline__ void resolve_inplace(const CompactArgs& a, int b, int
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = static_cast<int64_t>(tile) * tile_rows + u * rows_per_step + row_lane;
-    mv[u] = tile < n_tiles ? resolve_row(a, sbt, n_src, sbt, n_src, kp, n_tokens, i, word_off, col_ok)
-                           : RowMove{-1, -1};
+    mv[u] = live ? resolve_row(a, sbt, n_src, sbt, n_src, kp, n_tokens, i, word_off, col_ok) : RowMove{-1, -1};
   }
 }
 
-// In-place mode: a workgroup owns one column slice of one (layer, sequence)
-// and walks the rows in ascending tiles.  All loads of a tile complete before
-// the workgroup barrier, then its stores go out.  The rows of the next tile
-// are resolved (keep index -> page -> offset) while the current tile's words
-// are in flight; keep and the block tables are never written here.
+// In-place mode, hazard rows: a workgroup owns one column slice of one
+// (layer, sequence) and walks the hazard rows in ascending tiles.  All loads
+// of a tile complete before the workgroup barrier, then its stores go out.
+// The rows of the next tile are resolved (keep index -> page -> offset) while
+// the current tile's words are in flight; keep and the block tables are never
+// written here.
 template <typename Chunk>
 __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(CompactArgs a) {
   const int b = blockIdx.y;
@@ -235,11 +260,12 @@ __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(Compac
   const int64_t chunk = static_cast<int64_t>(slice) * slice_w + col;
   const bool col_ok = chunk < a.row_chunks;
   const int64_t word_off = chunk * static_cast<int64_t>(sizeof(Chunk));
-  const int n_tiles = (a.budget + tile_rows - 1) / tile_rows;
+  const int64_t* kp = a.keep + static_cast<int64_t>(b) * a.keep_stride;
 
+  bool live = hazard_tile(a, kp, 0, tile_rows);
   RowMove mv[kInplaceUnroll];
-  resolve_inplace(a, b, 0, n_tiles, tile_rows, rows_per_step, row_lane, word_off, col_ok, mv);
-  for (int tile = 0; tile < n_tiles; ++tile) {
+  resolve_inplace(a, b, 0, live, tile_rows, rows_per_step, row_lane, word_off, col_ok, mv);
+  for (int tile = 0; live; ++tile) {
     Chunk kv[kInplaceUnroll], vv[kInplaceUnroll];
 #pragma unroll
     for (int u = 0; u < kInplaceUnroll; ++u) {
@@ -248,8 +274,9 @@ __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(Compac
         vv[u] = *reinterpret_cast<KVC_GLOBAL const Chunk*>(vb + mv[u].src);
       }
     }
+    const bool live_next = hazard_tile(a, kp, tile + 1, tile_rows);
     RowMove next[kInplaceUnroll];
-    resolve_inplace(a, b, tile + 1, n_tiles, tile_rows, rows_per_step, row_lane, word_off, col_ok, next);
+    resolve_inplace(a, b, tile + 1, live_next, tile_rows, rows_per_step, row_lane, word_off, col_ok, next);
     // Every load of this tile has returned before any lane stores.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -261,6 +288,7 @@ __global__ __launch_bounds__(kInplaceThreads) void compact_inplace_kernel(Compac
       }
       mv[u] = next[u];
     }
+    live = live_next;
   }
 }
 
@@ -378,17 +406,26 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   while (word > 2 && ((ca.row_bytes % word) != 0 || (ca.page_stride_bytes % word) != 0)) word >>= 1;
   ca.row_chunks = ca.row_bytes / word;
 
-  // Column slice: whole rows (up to the workgroup width) in private mode;
-  // 256-byte slices in place, so enough independent workgroups fill the chip.
-  const int threads = inplace ? kInplaceThreads : kCopyThreads;
-  int64_t target = inplace ? (256 / word) : ca.row_chunks;
-  if (target > threads) target = threads;
-  int shift = 0;
-  while ((1 << shift) < target) ++shift;
-  ca.slice_shift = shift;
-  ca.n_slices = static_cast<int>(ceil_div(ca.row_chunks, int64_t(1) << shift));
+  // Column slice of `threads`-wide workgroups covering `target_chunks` words.
+  auto set_slices = [&](int threads, int64_t target_chunks) {
+    if (target_chunks > threads) target_chunks = threads;
+    int shift = 0;
+    while ((1 << shift) < target_chunks) ++shift;
+    ca.slice_shift = shift;
+    ca.n_slices = static_cast<int>(ceil_div(ca.row_chunks, int64_t(1) << shift));
+  };
+  // The row-parallel launch's grid, checked before anything is enqueued.
+  set_slices(kCopyThreads, ca.row_chunks);
+  const int copy_shift = ca.slice_shift, copy_slices = ca.n_slices;
+  const int tile_rows = (kCopyThreads >> copy_shift) * kCopyUnroll;
+  const int64_t gx = ceil_div(budget, tile_rows) * copy_slices * n_seq;
+  if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
   hipStream_t st = as_stream(stream);
   if (inplace) {
+    // Hazard rows first, in ordered walks over 256-byte column slices (enough
+    // independent workgroups to fill the chip); the safe rows follow below.
+    set_slices(kInplaceThreads, 256 / word);
+    ca.rows = kRowsHazard;
     dim3 grid(static_cast<unsigned>(ca.n_slices), static_cast<unsigned>(n_seq), static_cast<unsigned>(n_layers));
     switch (word) {
       case 16: compact_inplace_kernel<w128><<<grid, kInplaceThreads, 0, st>>>(ca); break;
@@ -396,13 +433,17 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
       case 4: compact_inplace_kernel<uint32_t><<<grid, kInplaceThreads, 0, st>>>(ca); break;
       default: compact_inplace_kernel<uint16_t><<<grid, kInplaceThreads, 0, st>>>(ca); break;
     }
-    return launch_status("kvc_compact");
+    const int rc = launch_status("kvc_compact");
+    if (rc != 0) return rc;
+    ca.rows = kRowsSafe;
+    ca.dst_off = src_block_offsets;
+    ca.dst_ids = src_block_ids;
+  } else {
+    ca.rows = kRowsAll;
   }
-  const int rows_per_step = kCopyThreads >> shift;
-  const int tile_rows = rows_per_step * kCopyUnroll;
-  const int64_t n_row_tiles = ceil_div(budget, tile_rows);
-  const int64_t gx = n_row_tiles * ca.n_slices * n_seq;
-  if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_compact: grid too large");
+  // Whole rows (up to the workgroup width) per workgroup.
+  ca.slice_shift = copy_shift;
+  ca.n_slices = copy_slices;
   dim3 grid(static_cast<unsigned>(gx));
   switch (word) {
     case 16: compact_private_kernel<w128><<<grid, kCopyThreads, 0, st>>>(ca); break;

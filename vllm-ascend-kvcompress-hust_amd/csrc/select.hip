@@ -6,9 +6,9 @@
 // them from the top, which pins the exact key T of the K-th largest score and
 // how many scores equal to T are still needed.  A last pass in index order
 // keeps every key > T plus the first `need` keys == T (ties go to the lowest
-// index): each thread owns a contiguous run of indices, and two workgroup
-// prefix sums give every run its ties and its first output slot, so the
-// output is sorted without a sort.
+// index), walking the segment in coalesced tiles: one workgroup prefix sum of
+// packed (greater, equal) counts per tile gives every key its output slot, so
+// the output is sorted without a sort.
 //
 // Segments follow select_keep_indices (tri/selection.py:108-196): the protected
 // prefix [0, prefix) and recent window [n-recent, n) are always kept; policy
@@ -24,6 +24,12 @@ namespace {
 constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelUnroll = 4;  // float4 words per thread in flight in a histogram pass
+#ifndef KVC_SEL_PEEL
+#define KVC_SEL_PEEL 1
+#endif
+constexpr int kSelPeel = KVC_SEL_PEEL;  // dominant digits counted with one atomic per wave
+constexpr int kEmitWords = 2;  // float4 words per thread per emission tile
+static_assert(kSelThreads * kEmitWords * 4 < 65536, "packed emission counts need 16 bits per half");
 
 struct SelectArgs {
   int n_seq, budget, prefix, recent, segments, policy;
@@ -112,6 +118,25 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
   return before + incl - v;
 }
 
+// Counts one key's digit into a wave's LDS histogram.  Scores of similar
+// magnitude share their high digits (the first pass sees little more than the
+// sign and exponent), so most lanes of a wave can hit one or two bins; up to
+// kSelPeel times, the lanes holding the first active lane's digit add their
+// number with a single atomic, and the lanes left count one by one.
+__device__ __forceinline__ void count_digit(uint32_t* hist, uint32_t digit) {
+#pragma unroll
+  for (int p = 0; p < kSelPeel; ++p) {
+    const uint32_t lead = __builtin_amdgcn_readfirstlane(digit);
+    const uint64_t same = __ballot(digit == lead);
+    if (digit == lead) {
+      if (__lane_id() == static_cast<unsigned>(__ffsll(static_cast<unsigned long long>(same)) - 1))
+        atomicAdd(&hist[lead], static_cast<uint32_t>(__popcll(same)));
+      return;
+    }
+  }
+  atomicAdd(&hist[digit], 1u);
+}
+
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
   __shared__ uint32_t whist[kSelWaves][256];
   __shared__ uint32_t hist[256];
@@ -170,7 +195,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
     __syncthreads();
     uint32_t* mine = whist[wave];
     for_each_key(sc, s.start, s.stop, [&](int64_t, uint32_t k) {
-      if ((k & mask) == want) atomicAdd(&mine[(k >> shift) & 255u], 1u);
+      if ((k & mask) == want) count_digit(mine, (k >> shift) & 255u);
     });
     __syncthreads();
     if (tid < 256) {
@@ -212,38 +237,72 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
   const uint32_t need_eq = need;  // keys equal to thresh that are kept
 
   // ---- ordered emission --------------------------------------------------
-  // Thread t owns the contiguous run [start + t*R, start + (t+1)*R): it counts
-  // its keys above and equal to the threshold, two workgroup scans give its
-  // ties to keep (the first need_eq ties in index order) and its first output
-  // slot, and it writes its kept indices in order.
-  const int64_t run = (len + kSelThreads - 1) / kSelThreads;
-  const int64_t r0 = min(s.start + tid * run, s.stop);
-  const int64_t r1 = min(r0 + run, s.stop);
-  uint32_t n_gt = 0, n_eq = 0;
-#pragma unroll 4
-  for (int64_t i = r0; i < r1; ++i) {
-    const uint32_t k = float_key(sc[i]);
-    n_gt += k > thresh;
-    n_eq += k == thresh;
-  }
-  uint32_t total;
-  const uint32_t eq_before = block_exclusive_scan(n_eq, s_wave, &total);
-  const uint32_t eq_take = eq_before >= need_eq ? 0u : min(n_eq, need_eq - eq_before);
-  uint32_t pos = block_exclusive_scan(n_gt + eq_take, s_wave, &total);
-  uint32_t eq_left = eq_take;
-#pragma unroll 4
-  for (int64_t i = r0; i < r1; ++i) {
-    const uint32_t k = float_key(sc[i]);
-    bool take = k > thresh;
-    if (k == thresh && eq_left > 0) {
-      take = true;
-      --eq_left;
+  // Key i is kept iff k > T, or k == T and fewer than need_eq ties precede it
+  // (ties go to the lowest index); its output slot is G(i) + min(E(i), need_eq),
+  // with G(i), E(i) the numbers of keys > T and == T before i in the segment.
+  // The segment is walked in tiles of kSelThreads * kEmitWords float4 words:
+  // thread t takes the tile's words [t*kEmitWords, (t+1)*kEmitWords), so the
+  // loads are coalesced and thread order is index order, and one workgroup scan
+  // of packed (G, E) counts per tile gives every thread its G and E.  The up to
+  // three keys before the first 16-byte boundary and after the last are counted
+  // by every thread and written by thread 0.
+  uint32_t g_run = 0, e_run = 0;  // G and E at the current position (uniform)
+  auto emit = [&](int64_t i, uint32_t k, uint32_t g, uint32_t e) {
+    if (k > thresh || (k == thresh && e < need_eq)) {
+      const int64_t slot = out_base + g + min(e, need_eq);
+      if (slot < a.budget) out[slot] = i;
     }
-    if (take) {
-      if (out_base + pos < a.budget) out[out_base + pos] = i;
-      ++pos;
+  };
+  auto serial = [&](int64_t i0, int64_t i1) {
+    for (int64_t i = i0; i < i1; ++i) {
+      const uint32_t k = float_key(sc[i]);
+      if (tid == 0) emit(i, k, g_run, e_run);
+      g_run += k > thresh;
+      e_run += k == thresh;
     }
+  };
+  const int64_t misalign = (reinterpret_cast<uintptr_t>(sc + s.start) >> 2) & 3;
+  const int64_t head = min((4 - misalign) & 3, len);
+  serial(s.start, s.start + head);
+  const int64_t body = s.start + head;
+  const int64_t n4 = (s.stop - body) >> 2;
+  const f32x4* v = reinterpret_cast<const f32x4*>(sc + body);
+  for (int64_t w0 = 0; w0 < n4; w0 += static_cast<int64_t>(kSelThreads) * kEmitWords) {
+    uint32_t k[kEmitWords][4];
+    bool valid[kEmitWords];
+    uint32_t g = 0, e = 0;
+#pragma unroll
+    for (int u = 0; u < kEmitWords; ++u) {
+      const int64_t w = w0 + static_cast<int64_t>(tid) * kEmitWords + u;
+      valid[u] = w < n4;
+      const f32x4 x = v[valid[u] ? w : n4 - 1];  // in range; surplus words are masked
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        k[u][q] = float_key(x[q]);
+        g += valid[u] && k[u][q] > thresh;
+        e += valid[u] && k[u][q] == thresh;
+      }
+    }
+    uint32_t tile_total;
+    // Per-tile counts stay below 2^16 (kSelThreads * kEmitWords * 4 keys), so
+    // the two halves of the packed sum never carry into each other.
+    const uint32_t before = block_exclusive_scan(g | (e << 16), s_wave, &tile_total);
+    uint32_t gb = g_run + (before & 0xFFFFu), eb = e_run + (before >> 16);
+#pragma unroll
+    for (int u = 0; u < kEmitWords; ++u) {
+      const int64_t i0 = body + 4 * (w0 + static_cast<int64_t>(tid) * kEmitWords + u);
+      if (!valid[u]) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        emit(i0 + q, k[u][q], gb, eb);
+        gb += k[u][q] > thresh;
+        eb += k[u][q] == thresh;
+      }
+    }
+    g_run += tile_total & 0xFFFFu;
+    e_run += tile_total >> 16;
   }
+  serial(body + 4 * n4, s.stop);
 }
 
 }  // namespace
