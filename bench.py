@@ -81,6 +81,12 @@ def parse_args() -> argparse.Namespace:
         help="only measure streaming read / write / copy ceilings of this GPU (4 GiB buffers)",
     )
     p.add_argument(
+        "--calibration",
+        action="store_true",
+        help="only measure calibration statistics (kvc_qstats_accumulate) over a Qwen2.5-14B-shaped calibration "
+        "pass: 48 layers of 4096-token bf16 query projections (40 heads x 128), one buffer per layer",
+    )
+    p.add_argument(
         "--placement-sweep",
         type=int,
         default=0,
@@ -212,6 +218,96 @@ def calibrate_copy(mib: int) -> int:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 3}), flush=True)
+    return 0
+
+
+def calibration_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -> int:
+    """Calibration statistics of one Qwen2.5-14B-shaped calibration pass per
+    step: every layer's projection [4096, 40*128] bf16 read once by
+    kvc_qstats_accumulate (distinct buffers, 2.0 GB in all, so no layer is
+    served from a cache); algorithmic bytes = the projections' bytes."""
+    import torch
+
+    from kvcompress_mi355x.calibration import LayerAccumulator
+
+    layers, tokens, heads, head_dim = 48, 4096, 40, 128
+    device = torch.device("cuda:0")
+    g = torch.Generator(device=device).manual_seed(0)
+    projections = [torch.randn(tokens, heads * head_dim, generator=g, device=device).to(torch.bfloat16) for _ in range(layers)]
+    accs = [LayerAccumulator(device=device) for _ in range(layers)]
+
+    def step() -> None:
+        for acc, q in zip(accs, projections):
+            acc.add(q, heads, head_dim, head_dim)
+
+    for _ in range(max(1, warmup)):
+        step()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    # Kernel time without the host's per-call work: the pass captured as one
+    # HIP graph (96 launches) and replayed.
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.graph(graph, stream=side):
+        step()
+    graph.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    device_ms = start.elapsed_time(end) / steps
+    nbytes = layers * tokens * heads * head_dim * 2
+    result = {
+        "metric": "calibration query statistics: projection tokens x layers / s; HBM GB/s",
+        "value": round(layers * tokens / wall, 1),
+        "unit": "token-layers/s",
+        "steps": steps,
+        "ms_per_step": round(1000 * wall, 4),
+        "graph_replay_ms_per_step": round(device_ms, 4),
+        "launch": "eager per-layer calls (value); roofline from one HIP graph of the pass",
+        "dtype": "bf16",
+        "config": {"workload": "qwen2.5-14b-calibration-pass", "layers": layers, "tokens": tokens, "heads": heads, "head_dim": head_dim},
+        "roofline": {
+            "kernel": "kvc_qstats_accumulate",
+            "bound": "hbm",
+            "achieved": round(nbytes / (device_ms / 1000) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(nbytes / (device_ms / 1000) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": nbytes,
+        },
+    }
+    if not no_cpu:
+        from oracle import calibration_ref as cref
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        sample = [q.cpu() for q in projections[:4]]
+
+        def cpu_step() -> float:
+            t = time.perf_counter()
+            for q in sample:
+                cref.QueryStatsAccumulator().add(q, heads, head_dim, head_dim)
+            return time.perf_counter() - t
+
+        cpu_step()
+        med = statistics.median(cpu_step() for _ in range(cpu_repeats))
+        result["cpu_baseline"] = {
+            "value": round(len(sample) * tokens / med, 1),
+            "unit": "token-layers/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"4 of 48 layers ({tokens} tokens each), torch float32 restatement; median of {cpu_repeats}",
+        }
+    print(json.dumps(result), flush=True)
     return 0
 
 
@@ -374,6 +470,8 @@ def main() -> int:
         return probe_bandwidth()
     if args.placement_sweep:
         return placement_sweep(args.config, args.placement_sweep)
+    if args.calibration:
+        return calibration_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1

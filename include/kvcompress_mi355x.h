@@ -43,7 +43,7 @@ typedef void* kvc_stream_t; /* hipStream_t */
 #define KVC_BLOCK_SIZE 128
 #define KVC_EINVAL (-22)
 
-enum kvc_dtype { KVC_DTYPE_BF16 = 0, KVC_DTYPE_FP16 = 1 };
+enum kvc_dtype { KVC_DTYPE_BF16 = 0, KVC_DTYPE_FP16 = 1, KVC_DTYPE_FP32 = 2 /* query statistics only */ };
 enum kvc_rope_style { KVC_ROPE_HALF = 0, KVC_ROPE_INTERLEAVED = 1 };
 enum kvc_policy { KVC_POLICY_GLOBAL = 0, KVC_POLICY_V3 = 1 };
 enum kvc_layer_aggregation { KVC_LAYER_MEAN = 0, KVC_LAYER_MAX = 1 };
@@ -253,6 +253,31 @@ int kvc_physical_slot_mapping(kvc_stream_t stream, int num_reqs, const int32_t* 
  * apply_physical_attention_lengths, pkg/provider.py:707-728). */
 int kvc_shift_lengths(kvc_stream_t stream, void* seq_lens, int elem_bytes, const int64_t* request_offsets,
                       int num_reqs);
+
+/* ----------------------------------------------------------- calibration -- */
+
+/* Query statistics of one layer's pre-RoPE query projections, accumulated over
+ * tokens (_LayerAccumulator.add, pkg/calibration.py:98-131).  Element (t, h, d)
+ * of q is at q[t*token_stride + h*head_dim + d] (dtype bf16, fp16 or fp32;
+ * token_stride >= heads*head_dim, e.g. 2*heads*head_dim for a q_proj whose
+ * output carries a gate after Q).  kvc_qstats_accumulate adds the tokens'
+ * partial sums into `state` (kvc_qstats_state_bytes bytes, zeroed by the
+ * caller before the first call); kvc_qstats_finish writes the totals over
+ * every call so far.  With F = rotary_dim/2 and P = head_dim - rotary_dim, for
+ * h < heads, f < F, p < P:
+ *   real_sum[h*F + f] = sum_t q(t, h, f)
+ *   imag_sum[h*F + f] = sum_t q(t, h, F + f)
+ *   abs_sum[h*F + f]  = sum_t sqrt(q(t, h, f)^2 + q(t, h, F + f)^2)
+ *   pass_sum[h*P + p] = sum_t q(t, h, rotary_dim + p)      (may be NULL if P == 0)
+ * Each term is the reference's float32 value; the sums are float64 in an
+ * order fixed by the shapes and the call sequence (identical on every run).
+ * The caller keeps the token count. */
+size_t kvc_qstats_state_bytes(int heads, int head_dim, int rotary_dim);
+int kvc_qstats_accumulate(kvc_stream_t stream, int dtype, const void* q, int64_t n_tokens,
+                          int64_t token_stride, int heads, int head_dim, int rotary_dim, void* state,
+                          size_t state_bytes);
+int kvc_qstats_finish(kvc_stream_t stream, int heads, int head_dim, int rotary_dim, const void* state,
+                      double* real_sum, double* imag_sum, double* abs_sum, double* pass_sum);
 
 /* ------------------------------------------------------- measurement -- */
 

@@ -11,6 +11,10 @@ Modules
   brute             float64 brute force (plain loops / numpy) used to pin the
                     restatement on small inputs, and the deterministic
                     (score desc, index asc) selection rule.
+  calibration_ref   torch-CPU restatement of the calibration generator's query
+                    statistics (_LayerAccumulator.add, pkg/calibration.py:98-131,
+                    and the per-layer means of :351-371) with a float64 loop
+                    brute force of the definitions.
 
 Parity pins (how each oracle function is checked, see tests/test_oracle_*.py):
   build_geometric_offsets   closed form 2^k <= max
@@ -30,6 +34,10 @@ Parity pins (how each oracle function is checked, see tests/test_oracle_*.py):
                             tests/test_provider_integration.py:486-514)
   physical_seq_lens         reference KAT ([301,21] -> [129,21],
                             tests/test_provider_integration.py:486-514)
+  QueryStatsAccumulator     closed forms ((3,4) pairs -> means 3, 4, |q| 5;
+                            half-style pair layout; gate half ignored; head-shaped
+                            input equals flat); float64 loop brute force
+                            (tests/test_oracle_calibration.py)
   brute.slot_mapping        closed form slot = table[p // 128] * 128 + p % 128
                             (block-table arithmetic of tri/cache.py:9-15) on
                             hand-worked cases; the GPU kernel is checked against it

@@ -18,6 +18,7 @@ ABI_VERSION = 1
 EINVAL = -22
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
+DTYPE_FP32 = 2
 ROPE_HALF = 0
 ROPE_INTERLEAVED = 1
 POLICY_GLOBAL = 0
@@ -68,6 +69,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_shift_positions": (_i32, [_p, _p, _p, _i32, _p, _i64, _p]),
     "kvc_physical_slot_mapping": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i64, _p, _p]),
     "kvc_shift_lengths": (_i32, [_p, _p, _i32, _p, _i32]),
+    "kvc_qstats_state_bytes": (_sz, [_i32, _i32, _i32]),
+    "kvc_qstats_accumulate": (_i32, [_p, _i32, _p, _i64, _i64, _i32, _i32, _i32, _p, _sz]),
+    "kvc_qstats_finish": (_i32, [_p, _i32, _i32, _i32, _p, _p, _p, _p, _p]),
     "kvc_bandwidth_probe": (_i32, [_p, _i32, _i32, _p, _p, _i64, _i32]),
 }
 
