@@ -169,6 +169,21 @@ int kvc_select_keep(kvc_stream_t stream, int n_seq, int max_seq_len, const int32
                     int protected_prefix, int protected_recent, int segments, int policy,
                     int64_t* keep, int64_t keep_stride);
 
+/* The same selection with each (sequence, segment) cut into chunks of at least
+ * 4096 scores, one workgroup per chunk (seven launches: reset, four radix
+ * passes, per-chunk counts, emission), for batches of a few long sequences
+ * that one workgroup per sequence would leave on a few CUs.  Identical output
+ * to kvc_select_keep.  No counterpart in the reference beyond
+ * select_keep_indices itself.  `workspace`: at least
+ * kvc_select_workspace_bytes(n_seq, segments, policy) bytes, 16-byte aligned,
+ * any contents (the first launch resets it); max_seq_len must bound every
+ * sequence length. */
+size_t kvc_select_workspace_bytes(int n_seq, int segments, int policy);
+int kvc_select_keep_split(kvc_stream_t stream, int n_seq, int max_seq_len, const int32_t* seq_lens,
+                          const int64_t* token_offsets, const float* scores, int budget,
+                          int protected_prefix, int protected_recent, int segments, int policy,
+                          int64_t* keep, int64_t keep_stride, void* workspace, size_t workspace_bytes);
+
 /* ------------------------------------------------------------ compaction -- */
 
 /* Move the kept K and V rows of every layer into their destinations

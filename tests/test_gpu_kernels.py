@@ -268,6 +268,92 @@ def test_select_matches_stable_brute_force(hip_device, case) -> None:
         assert torch.equal(keep, oracle)
 
 
+def _stable_keep_np(scores: np.ndarray, budget: int, prefix: int, recent: int, segments: int, policy: str) -> np.ndarray:
+    """brute.select_stable's rule (higher order key first, then lower index),
+    vectorised for long inputs: the same protected windows and v3 quotas."""
+    bits = scores.astype(np.float32).view(np.uint32).astype(np.int64)
+    keys = np.where(bits & 0x80000000, (~bits) & 0xFFFFFFFF, bits | 0x80000000)
+    n = scores.shape[0]
+    prefix = min(prefix, n)
+    recent = min(recent, n - prefix)
+    keep = [np.arange(prefix), np.arange(n - recent, n)]
+
+    def top(lo: int, hi: int, k: int) -> np.ndarray:
+        idx = np.arange(lo, hi)
+        order = np.lexsort((idx, -keys[lo:hi]))
+        return idx[order[:k]]
+
+    mc = n - prefix - recent
+    if policy == "global":
+        keep.append(top(prefix, n - recent, budget - prefix - recent))
+    else:
+        evict = n - budget
+        for s in range(segments):
+            a = prefix + mc * s // segments
+            b = prefix + mc * (s + 1) // segments
+            if b > a:
+                quota = (b - a) - (evict * (b - prefix) // mc - evict * (a - prefix) // mc)
+                keep.append(top(a, b, max(quota, 0)))
+    return np.sort(np.concatenate(keep)).astype(np.int64)
+
+
+SPLIT_BATCHES = [
+    # (lengths, budget, prefix, recent, segments, policy)
+    ((300001, 70000, 4097, 40000, 131072), 4096, 0, 128, 8, "global"),
+    ((600003, 300000), 4608, 128, 512, 8, "v3"),
+    ((4224, 8191), 4096, 0, 128, 8, "global"),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_BATCHES, ids=["global-ragged", "v3-long", "global-short"])
+@pytest.mark.parametrize("ties", [False, True])
+def test_select_split_matches_single_and_brute_force(hip_device, case, ties) -> None:
+    _, selection, _ = _kvc()
+    lens, budget, prefix, recent, segments, policy = case
+    g = torch.Generator().manual_seed(sum(lens) + ties)
+    scores = torch.randn(sum(lens), generator=g)
+    if ties:
+        scores = torch.round(scores * 4) / 4
+        specials = torch.randint(0, sum(lens), (64,), generator=g)
+        scores[specials[:16]] = float("nan")
+        scores[specials[16:32]] = float("inf")
+        scores[specials[32:48]] = float("-inf")
+        scores[specials[48:]] = -0.0
+    offsets = [0]
+    for n in lens:
+        offsets.append(offsets[-1] + n)
+    d_scores = scores.to(hip_device)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=hip_device)
+    token_offsets = torch.tensor(offsets, dtype=torch.int64, device=hip_device)
+    kw = dict(budget=budget, protected_prefix=prefix, protected_recent=recent, segments=segments, policy=policy)
+    single = torch.full((len(lens), budget + 3), -7, dtype=torch.int64, device=hip_device)
+    split = torch.full_like(single, -7)
+    selection.select_keep_indices_batched(d_scores, seq_lens, token_offsets, list(lens), single, shape="single", **kw)
+    ws = selection.select_workspace(len(lens), segments, policy, hip_device)
+    ws.fill_(0xAB)  # any contents: the first launch resets the scratch
+    for _ in range(2):  # the second call reuses the workspace left by the first
+        selection.select_keep_indices_batched(d_scores, seq_lens, token_offsets, list(lens), split, shape="split", workspace=ws, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(split, single)
+    assert bool((split[:, budget:] == -7).all()), "entries past the budget must stay untouched"
+    for b, n in enumerate(lens):
+        want = _stable_keep_np(scores[offsets[b] : offsets[b + 1]].numpy(), budget, prefix, recent, segments, policy)
+        np.testing.assert_array_equal(split[b, :budget].cpu().numpy(), want)
+
+
+def test_select_split_rejects_a_small_workspace(hip_device) -> None:
+    _, selection, _ = _kvc()
+    scores = torch.randn(50000, device=hip_device)
+    lens = torch.tensor([50000], dtype=torch.int32, device=hip_device)
+    offs = torch.tensor([0, 50000], dtype=torch.int64, device=hip_device)
+    keep = torch.empty((1, 4096), dtype=torch.int64, device=hip_device)
+    small = torch.empty(64, dtype=torch.uint8, device=hip_device)
+    with pytest.raises(ValueError, match="workspace"):
+        selection.select_keep_indices_batched(scores, lens, offs, [50000], keep, budget=4096, protected_prefix=0,
+                                              protected_recent=128, segments=8, policy="global", shape="split",
+                                              workspace=small)
+
+
 def test_select_special_values(hip_device) -> None:
     _, selection, _ = _kvc()
     scores = torch.tensor([0.0, -0.0, float("nan"), float("inf"), 1.0, 1.0, float("-inf"), -3.0])

@@ -9,6 +9,7 @@ TriAttentionMethod._select_keep_indices and compress (tri/method.py:256-475):
   3. head statistics  kvc_head_stats       mean/var [S, n_seq, H_q]
   4. aggregate        kvc_aggregate        agg [sum N] (head max, layer mean, sanitise)
   5. select           kvc_select_keep      keep [n_seq, budget] ascending
+                      (kvc_select_keep_split for a few long sequences)
   6. compact          kvc_compact          kept K/V rows of every layer
   7. block tables     kvc_rewrite_block_tables
 
@@ -31,7 +32,7 @@ import torch
 from ... import _native
 from . import _device as dev
 from .cache import compact_layers, rewrite_block_tables
-from .selection import POLICY_CODES, validate_selection
+from .selection import POLICY_CODES, prefers_split, select_keep_indices_batched, select_workspace, validate_selection
 
 
 @dataclass(frozen=True)
@@ -211,6 +212,7 @@ class CompressionPipeline:
         self.protected_recent = int(protected_recent)
         self.segments = int(segments)
         self.policy = policy
+        self.select_shape = "auto"  # "auto", "single" or "split" (kvc_select_keep / _split)
         self.layer_aggregation = layer_aggregation
         self.n_heads = tables.kv_heads * tables.qpk
         self.scoring_ptrs = dev.pointer_table(scoring_k_caches, self.device)
@@ -247,6 +249,7 @@ class CompressionPipeline:
         self.var = torch.empty_like(self.mean)
         self.agg = torch.empty(self.max_tokens, dtype=torch.float32, device=dev_)
         self.keep = torch.empty((self.max_seqs, self.budget), dtype=torch.int64, device=dev_)
+        self.select_ws = select_workspace(self.max_seqs, self.segments, self.policy, dev_)
         ws = _native.load().kvc_score_workspace_bytes(
             s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len
         )
@@ -389,21 +392,30 @@ class CompressionPipeline:
         )
 
     def select(self, batch: Batch) -> torch.Tensor:
-        _native.call(
-            "kvc_select_keep",
-            dev.stream_handle(self.device),
-            batch.n_seq,
-            max(batch.seq_lens_host),
-            dev.ptr(batch.seq_lens),
-            dev.ptr(batch.token_offsets),
-            dev.ptr(self.agg),
-            self.budget,
-            self.protected_prefix,
-            self.protected_recent,
-            self.segments,
-            POLICY_CODES[self.policy],
-            dev.ptr(self.keep),
-            int(self.keep.stride(0)),
+        shape = self.select_shape
+        if shape == "auto":
+            split = prefers_split(
+                batch.seq_lens_host,
+                protected_prefix=self.protected_prefix,
+                protected_recent=self.protected_recent,
+                segments=self.segments,
+                policy=self.policy,
+            )
+            shape = "split" if split else "single"
+        select_keep_indices_batched(
+            self.agg,
+            batch.seq_lens,
+            batch.token_offsets,
+            batch.seq_lens_host,
+            self.keep,
+            budget=self.budget,
+            protected_prefix=self.protected_prefix,
+            protected_recent=self.protected_recent,
+            segments=self.segments,
+            policy=self.policy,
+            shape=shape,
+            workspace=self.select_ws,
+            validate=False,  # select_step and the callers of select validate the batch first
         )
         return self.keep[: batch.n_seq]
 

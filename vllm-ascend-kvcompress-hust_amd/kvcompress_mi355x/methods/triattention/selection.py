@@ -16,6 +16,27 @@ from . import _device as dev
 
 POLICY_CODES = {"global": _native.POLICY_GLOBAL, "v3": _native.POLICY_V3}
 
+# kvc_select_keep runs one workgroup per (sequence, segment), about 10 us plus
+# 0.7 us per 1K scores of the longest segment; kvc_select_keep_split (seven
+# launches, chunks spread over the chip) takes 50-65 us for up to a few dozen
+# segments: 4 x 130816 scores 66 us against 100 us, 16 x 16256 53 us against
+# 23 us.  The crossover is near 64K scores per segment.
+SPLIT_MIN_SEGMENT = 65536
+SPLIT_MAX_JOBS = 32
+
+
+def prefers_split(seq_lens_host: list[int], *, protected_prefix: int, protected_recent: int, segments: int, policy: str) -> bool:
+    """Whether the chunked launch shape suits this batch: few jobs, long segments."""
+    per_seq = segments if policy == "v3" else 1
+    longest = max(seq_lens_host) - protected_prefix - protected_recent
+    return len(seq_lens_host) * per_seq <= SPLIT_MAX_JOBS and longest // per_seq >= SPLIT_MIN_SEGMENT
+
+
+def select_workspace(n_seq: int, segments: int, policy: str, device: torch.device) -> torch.Tensor:
+    """Scratch of the chunked launch shape for up to ``n_seq`` sequences."""
+    size = int(_native.load().kvc_select_workspace_bytes(n_seq, segments, POLICY_CODES[policy]))
+    return torch.empty(max(size, 16), dtype=torch.uint8, device=device)
+
 
 def validate_selection(
     token_count: int, *, budget: int, protected_prefix: int, protected_recent: int, segments: int, policy: str
@@ -61,26 +82,22 @@ def select_keep_indices(
     )
     values = scores.to(dtype=torch.float32).contiguous()
     device = values.device
-    keep = torch.empty(budget, dtype=torch.int64, device=device)
+    keep = torch.empty((1, budget), dtype=torch.int64, device=device)
     seq_lens = torch.tensor([token_count], dtype=torch.int32, device=device)
     token_offsets = torch.tensor([0, token_count], dtype=torch.int64, device=device)
-    _native.call(
-        "kvc_select_keep",
-        dev.stream_handle(device),
-        1,
-        token_count,
-        dev.ptr(seq_lens),
-        dev.ptr(token_offsets),
-        dev.ptr(values),
-        int(budget),
-        int(protected_prefix),
-        int(protected_recent),
-        int(segments),
-        POLICY_CODES[policy],
-        dev.ptr(keep),
-        int(budget),
+    select_keep_indices_batched(
+        values,
+        seq_lens,
+        token_offsets,
+        [token_count],
+        keep,
+        budget=budget,
+        protected_prefix=protected_prefix,
+        protected_recent=protected_recent,
+        segments=segments,
+        policy=policy,
     )
-    return keep
+    return keep[0]
 
 
 def select_keep_indices_batched(
@@ -95,9 +112,18 @@ def select_keep_indices_batched(
     protected_recent: int,
     segments: int,
     policy: str,
+    shape: str = "auto",
+    workspace: torch.Tensor | None = None,
+    validate: bool = True,
 ) -> torch.Tensor:
-    """All sequences of a batch in one launch; ``keep`` is int64 [n_seq, >= budget]."""
-    for n in seq_lens_host:
+    """All sequences of a batch at once; ``keep`` is int64 [n_seq, >= budget].
+
+    ``shape``: "auto" (``prefers_split``), "single" (one workgroup per
+    sequence segment) or "split" (chunked; ``workspace`` from
+    ``select_workspace``, allocated here when None).  Both shapes return the
+    same indices.  ``validate=False`` skips the per-sequence host checks for a
+    caller that has made them already."""
+    for n in seq_lens_host if validate else ():
         validate_selection(
             n,
             budget=budget,
@@ -109,8 +135,14 @@ def select_keep_indices_batched(
     n_seq = len(seq_lens_host)
     if keep.ndim != 2 or keep.shape[0] < n_seq or keep.shape[1] < budget or keep.stride(1) != 1:
         raise ValueError("keep must be int64 [n_seq, >= budget] with contiguous rows")
-    _native.call(
-        "kvc_select_keep",
+    if shape not in ("auto", "single", "split"):
+        raise ValueError(f"unknown selection launch shape {shape!r}")
+    if shape == "auto":
+        shape = "split" if prefers_split(
+            seq_lens_host, protected_prefix=protected_prefix, protected_recent=protected_recent,
+            segments=segments, policy=policy,
+        ) else "single"
+    args = (
         dev.stream_handle(scores.device),
         n_seq,
         max(seq_lens_host),
@@ -125,4 +157,10 @@ def select_keep_indices_batched(
         dev.ptr(keep),
         int(keep.stride(0)),
     )
+    if shape == "single":
+        _native.call("kvc_select_keep", *args)
+        return keep
+    if workspace is None:
+        workspace = select_workspace(n_seq, segments, policy, scores.device)
+    _native.call("kvc_select_keep_split", *args, dev.ptr(workspace), int(workspace.numel()))
     return keep
