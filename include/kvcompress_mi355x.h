@@ -152,6 +152,26 @@ int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int n_seq, int
                   const float* mean, const float* var, int64_t stats_layer_stride,
                   int64_t stats_seq_stride, int layer_aggregation, unsigned flags, float* agg);
 
+/* Tensor-parallel halves of kvc_aggregate (the reference's TP path,
+ * tri/method.py:316-322,447-461 with _aggregate_torch's defer_tp_reduce,
+ * :477-503).  A rank holding a shard of the KV heads scores and normalises its
+ * own query heads, writes each scoring layer's head maximum
+ *   layer_scores[l*layer_stride + token_offsets[b] + t] = max_h z   (NaN-propagating)
+ * with kvc_layer_head_max (flags: KVC_AGG_RSQRT only), the ranks reduce
+ * layer_scores with an elementwise MAX (all_reduce(MAX) over the TP group; not
+ * part of this library), and kvc_combine_layer_scores turns the reduced layer
+ * scores into the aggregate: layers combined in layer order (copy, then + or
+ * max), then KVC_AGG_FINALIZE's division and NaN/inf mapping if set.  With
+ * every head on one rank the result equals kvc_aggregate's bit for bit. */
+int kvc_layer_head_max(kvc_stream_t stream, int n_layers, int n_heads, int n_seq, int max_seq_len,
+                       const int32_t* seq_lens, const int64_t* token_offsets, const float* raw,
+                       int64_t raw_layer_stride, int64_t raw_token_stride, int64_t raw_head_stride,
+                       const float* mean, const float* var, int64_t stats_layer_stride,
+                       int64_t stats_seq_stride, unsigned flags, float* layer_scores,
+                       int64_t layer_stride);
+int kvc_combine_layer_scores(kvc_stream_t stream, int n_layers, int64_t n_tokens, const float* layer_scores,
+                             int64_t layer_stride, int layer_aggregation, unsigned flags, float* agg);
+
 /* ------------------------------------------------------------- selection -- */
 
 /* Sorted keep indices of every sequence (select_keep_indices,

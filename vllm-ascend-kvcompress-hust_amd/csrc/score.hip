@@ -399,6 +399,7 @@ struct AggArgs {
   const float* var;
   int64_t stats_layer_stride, stats_seq_stride;
   float* agg;
+  int64_t layer_out_stride;  // 0: combine layers into agg; else layer l's head maxima at agg + l*stride
 };
 
 __device__ __forceinline__ float normalise(float s, float mean, float scale, bool rsqrt_form) {
@@ -417,13 +418,17 @@ __device__ __forceinline__ float combine_layers(float total, float best, int l, 
   return (a.layer_mode == KVC_LAYER_MEAN) ? total + best : max_nan(total, best);
 }
 
-__device__ __forceinline__ float finalize(float total, const AggArgs& a) {
-  if (a.flags & KVC_AGG_FINALIZE) {
-    if (a.layer_mode == KVC_LAYER_MEAN) total = total / static_cast<float>(a.n_layers);
+__device__ __forceinline__ float finalize_total(float total, unsigned flags, int layer_mode, int n_layers) {
+  if (flags & KVC_AGG_FINALIZE) {
+    if (layer_mode == KVC_LAYER_MEAN) total = total / static_cast<float>(n_layers);
     if (total != total) total = -INFINITY;
     else if (total == INFINITY) total = 1e30f;
   }
   return total;
+}
+
+__device__ __forceinline__ float finalize(float total, const AggArgs& a) {
+  return finalize_total(total, a.flags, a.layer_mode, a.n_layers);
 }
 
 __device__ void load_layer_stats(const AggArgs& a, int b, float* s_mean, float* s_scale) {
@@ -475,9 +480,13 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
       }
     }
     best = quad_max_nan(best);
+    if (a.layer_out_stride) {
+      if (valid && q == 0) a.agg[l * a.layer_out_stride + tok] = best;
+      continue;
+    }
     total = combine_layers(total, best, l, a, tok);
   }
-  if (valid && q == 0) a.agg[tok] = finalize(total, a);
+  if (valid && q == 0 && !a.layer_out_stride) a.agg[tok] = finalize(total, a);
 }
 
 // Head-major scores (unit token stride): one lane per token, so every load of
@@ -516,9 +525,32 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_tokens_kernel(AggArgs a
       }
       for (; h < a.n_heads; ++h) best = max_nan(best, normalise(col[h * a.raw_head_stride], lm[h], ls[h], rsqrt_form));
     }
+    if (a.layer_out_stride) {
+      if (valid) a.agg[l * a.layer_out_stride + tok] = best;
+      continue;
+    }
     total = combine_layers(total, best, l, a, tok);
   }
-  if (valid) a.agg[tok] = finalize(total, a);
+  if (valid && !a.layer_out_stride) a.agg[tok] = finalize(total, a);
+}
+
+// Layer scores [n_layers][stride] -> aggregate: layers combined in layer order
+// (copy, then + or NaN-propagating max), as the fused aggregate does.
+__global__ void combine_layer_scores_kernel(int n_layers, int64_t n_tokens, const float* __restrict__ layer_scores,
+                                            int64_t layer_stride, int layer_mode, unsigned flags, float* agg) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n_tokens) return;
+  float total = 0.0f;
+  for (int l = 0; l < n_layers; ++l) {
+    const float v = layer_scores[l * layer_stride + t];
+    if (l == 0) {
+      total = v;
+      if (flags & KVC_AGG_ACCUMULATE) total = (layer_mode == KVC_LAYER_MEAN) ? agg[t] + v : max_nan(agg[t], v);
+    } else {
+      total = (layer_mode == KVC_LAYER_MEAN) ? total + v : max_nan(total, v);
+    }
+  }
+  agg[t] = finalize_total(total, flags, layer_mode, n_layers);
 }
 
 using ScoreKernelFn = void (*)(ScoreArgs);
@@ -727,23 +759,22 @@ extern "C" int kvc_head_stats(kvc_stream_t stream, int n_layers, int kv_heads, i
   return launch_status("kvc_head_stats");
 }
 
-extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int n_seq,
-                             int max_seq_len, const int32_t* seq_lens,
-                             const int64_t* token_offsets, const float* raw,
-                             int64_t raw_layer_stride, int64_t raw_token_stride,
-                             int64_t raw_head_stride, const float* mean, const float* var,
-                             int64_t stats_layer_stride, int64_t stats_seq_stride,
-                             int layer_aggregation, unsigned flags, float* agg) {
+namespace kvc {
+namespace {
+
+int launch_aggregate(const char* who, kvc_stream_t stream, int n_layers, int n_heads, int n_seq, int max_seq_len,
+                     const int32_t* seq_lens, const int64_t* token_offsets, const float* raw,
+                     int64_t raw_layer_stride, int64_t raw_token_stride, int64_t raw_head_stride, const float* mean,
+                     const float* var, int64_t stats_layer_stride, int64_t stats_seq_stride, int layer_aggregation,
+                     unsigned flags, float* out, int64_t layer_out_stride) {
   if (n_layers <= 0 || n_heads <= 0 || n_seq <= 0 || max_seq_len < 0)
-    return fail(KVC_EINVAL, "kvc_aggregate: sizes must be positive");
+    return fail(KVC_EINVAL, "%s: sizes must be positive", who);
   if (n_layers * n_heads > kAggMaxStats)
-    return fail(KVC_EINVAL, "kvc_aggregate: layers*heads %d exceeds %d", n_layers * n_heads,
-                kAggMaxStats);
+    return fail(KVC_EINVAL, "%s: layers*heads %d exceeds %d", who, n_layers * n_heads, kAggMaxStats);
   if (layer_aggregation != KVC_LAYER_MEAN && layer_aggregation != KVC_LAYER_MAX)
-    return fail(KVC_EINVAL, "kvc_aggregate: unknown layer aggregation %d", layer_aggregation);
-  if (!seq_lens || !token_offsets || !raw || !mean || !var || !agg)
-    return fail(KVC_EINVAL, "kvc_aggregate: null pointer");
-  if (n_seq > 65535) return fail(KVC_EINVAL, "kvc_aggregate: too many sequences");
+    return fail(KVC_EINVAL, "%s: unknown layer aggregation %d", who, layer_aggregation);
+  if (!seq_lens || !token_offsets || !raw || !mean || !var || !out) return fail(KVC_EINVAL, "%s: null pointer", who);
+  if (n_seq > 65535) return fail(KVC_EINVAL, "%s: too many sequences", who);
   if (max_seq_len == 0) return 0;
   AggArgs aa;
   aa.n_layers = n_layers;
@@ -761,14 +792,56 @@ extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int
   aa.var = var;
   aa.stats_layer_stride = stats_layer_stride;
   aa.stats_seq_stride = stats_seq_stride;
-  aa.agg = agg;
+  aa.agg = out;
+  aa.layer_out_stride = layer_out_stride;
   const size_t lds = static_cast<size_t>(2) * n_layers * n_heads * sizeof(float);
   if (raw_token_stride == 1) {
     dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggThreads)), static_cast<unsigned>(n_seq));
     aggregate_tokens_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
-    return launch_status("kvc_aggregate");
+    return launch_status(who);
   }
   dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggTokensPerBlock)), static_cast<unsigned>(n_seq));
   aggregate_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
-  return launch_status("kvc_aggregate");
+  return launch_status(who);
+}
+
+}  // namespace
+}  // namespace kvc
+
+extern "C" int kvc_aggregate(kvc_stream_t stream, int n_layers, int n_heads, int n_seq,
+                             int max_seq_len, const int32_t* seq_lens,
+                             const int64_t* token_offsets, const float* raw,
+                             int64_t raw_layer_stride, int64_t raw_token_stride,
+                             int64_t raw_head_stride, const float* mean, const float* var,
+                             int64_t stats_layer_stride, int64_t stats_seq_stride,
+                             int layer_aggregation, unsigned flags, float* agg) {
+  return launch_aggregate("kvc_aggregate", stream, n_layers, n_heads, n_seq, max_seq_len, seq_lens, token_offsets,
+                          raw, raw_layer_stride, raw_token_stride, raw_head_stride, mean, var, stats_layer_stride,
+                          stats_seq_stride, layer_aggregation, flags, agg, 0);
+}
+
+extern "C" int kvc_layer_head_max(kvc_stream_t stream, int n_layers, int n_heads, int n_seq, int max_seq_len,
+                                  const int32_t* seq_lens, const int64_t* token_offsets, const float* raw,
+                                  int64_t raw_layer_stride, int64_t raw_token_stride, int64_t raw_head_stride,
+                                  const float* mean, const float* var, int64_t stats_layer_stride,
+                                  int64_t stats_seq_stride, unsigned flags, float* layer_scores,
+                                  int64_t layer_stride) {
+  if (layer_stride <= 0) return fail(KVC_EINVAL, "kvc_layer_head_max: layer_stride must be positive");
+  return launch_aggregate("kvc_layer_head_max", stream, n_layers, n_heads, n_seq, max_seq_len, seq_lens,
+                          token_offsets, raw, raw_layer_stride, raw_token_stride, raw_head_stride, mean, var,
+                          stats_layer_stride, stats_seq_stride, KVC_LAYER_MEAN, flags & KVC_AGG_RSQRT, layer_scores,
+                          layer_stride);
+}
+
+extern "C" int kvc_combine_layer_scores(kvc_stream_t stream, int n_layers, int64_t n_tokens, const float* layer_scores,
+                                        int64_t layer_stride, int layer_aggregation, unsigned flags, float* agg) {
+  if (n_layers <= 0 || n_tokens < 0 || layer_stride < n_tokens)
+    return fail(KVC_EINVAL, "kvc_combine_layer_scores: bad sizes");
+  if (layer_aggregation != KVC_LAYER_MEAN && layer_aggregation != KVC_LAYER_MAX)
+    return fail(KVC_EINVAL, "kvc_combine_layer_scores: unknown layer aggregation %d", layer_aggregation);
+  if (n_tokens == 0) return 0;
+  if (!layer_scores || !agg) return fail(KVC_EINVAL, "kvc_combine_layer_scores: null pointer");
+  combine_layer_scores_kernel<<<static_cast<unsigned>(ceil_div(n_tokens, 256)), 256, 0, as_stream(stream)>>>(
+      n_layers, n_tokens, layer_scores, layer_stride, layer_aggregation, flags, agg);
+  return launch_status("kvc_combine_layer_scores");
 }

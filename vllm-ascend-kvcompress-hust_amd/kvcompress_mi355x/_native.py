@@ -57,6 +57,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i32, _u32, _p],
     ),
+    "kvc_layer_head_max": (
+        _i32,
+        [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _u32, _p, _i64],
+    ),
+    "kvc_combine_layer_scores": (_i32, [_p, _i32, _i64, _p, _i64, _i32, _u32, _p]),
     "kvc_select_keep": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i64]),
     "kvc_select_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "kvc_select_keep_split": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _sz]),

@@ -250,6 +250,7 @@ class CompressionPipeline:
         self.agg = torch.empty(self.max_tokens, dtype=torch.float32, device=dev_)
         self.keep = torch.empty((self.max_seqs, self.budget), dtype=torch.int64, device=dev_)
         self.select_ws = select_workspace(self.max_seqs, self.segments, self.policy, dev_)
+        self.layer_scores = None  # [S, max_tokens] per-layer head maxima, made on first use
         ws = _native.load().kvc_score_workspace_bytes(
             s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len
         )
@@ -390,6 +391,75 @@ class CompressionPipeline:
             _native.AGG_FINALIZE,
             dev.ptr(self.agg),
         )
+
+    # ---------------------------------------------- tensor-parallel halves --
+    def local_layer_scores(self, batch: Batch) -> torch.Tensor:
+        """Per-layer head maxima over this pipeline's query heads, [S, sum N]
+        (after ``score``): the tensor the reference's TP path all-reduces with
+        MAX across the ranks that hold the other KV heads
+        (tri/method.py:316-322,447-461).  Rewritten by every call."""
+        t = self.tables
+        total = batch.total_tokens
+        if self.layer_scores is None or self.layer_scores.shape[1] < total:
+            self.layer_scores = torch.empty((t.n_layers, self.max_tokens), dtype=torch.float32, device=self.device)
+        _native.call(
+            "kvc_layer_head_max",
+            dev.stream_handle(self.device),
+            t.n_layers,
+            self.n_heads,
+            batch.n_seq,
+            max(batch.seq_lens_host),
+            dev.ptr(batch.seq_lens),
+            dev.ptr(batch.token_offsets),
+            dev.ptr(self.raw),
+            *self.raw_strides(),
+            dev.ptr(self.mean),
+            dev.ptr(self.var),
+            batch.n_seq * self.n_heads,
+            self.n_heads,
+            0,
+            dev.ptr(self.layer_scores),
+            int(self.layer_scores.stride(0)),
+        )
+        return self.layer_scores[:, :total]
+
+    def combine_layer_scores(self, batch: Batch, layer_scores: torch.Tensor) -> None:
+        """The aggregate from layer scores reduced across the TP group: layers
+        combined in order, mean division and nan_to_num (tri/method.py:455-467)."""
+        if layer_scores.ndim != 2 or layer_scores.shape[0] != self.tables.n_layers or layer_scores.stride(1) != 1:
+            raise ValueError("layer scores must be [scoring layers, tokens] with contiguous rows")
+        _native.call(
+            "kvc_combine_layer_scores",
+            dev.stream_handle(self.device),
+            self.tables.n_layers,
+            batch.total_tokens,
+            dev.ptr(layer_scores),
+            int(layer_scores.stride(0)),
+            _native.LAYER_MEAN if self.layer_aggregation == "mean" else _native.LAYER_MAX,
+            _native.AGG_FINALIZE,
+            dev.ptr(self.agg),
+        )
+
+    def step_sharded(self, batch: Batch, all_reduce_max, *, rewrite: bool = True):
+        """The step of one tensor-parallel rank whose caches and calibration
+        tables hold a shard of the KV heads: score the local heads, reduce the
+        per-layer head maxima with ``all_reduce_max(tensor)`` (an in-place
+        elementwise MAX over the group, e.g. torch.distributed.all_reduce with
+        ReduceOp.MAX on a RCCL group; the library itself issues no collective),
+        then select on the shared aggregate and compact the local heads.  Every
+        rank of the group gets the same keep indices."""
+        self.validate(batch)
+        self.ensure_capacity(batch)
+        self.score(batch)
+        scores = self.local_layer_scores(batch)
+        all_reduce_max(scores)
+        self.combine_layer_scores(batch, scores)
+        keep = self.select(batch)
+        self.compact(batch)
+        if not rewrite:
+            return keep, None, None
+        tables, freed = self.rewrite(batch)
+        return keep, tables, freed
 
     def select(self, batch: Batch) -> torch.Tensor:
         shape = self.select_shape
