@@ -82,7 +82,15 @@ def test_kv_head_shards_reproduce_the_unsharded_step(hip_device, config, overrid
     reduced = torch.maximum(local[0], local[1])
     near = 0
     for r, (pipeline, ks, vs) in enumerate(shards):
-        keep, tables, freed = pipeline.step_sharded(batch, lambda t: t.copy_(reduced))
+        calls = []
+
+        def all_reduce_max(t: torch.Tensor) -> None:
+            calls.append(tuple(t.shape))
+            t.copy_(reduced)
+
+        keep, tables, freed = pipeline.step_sharded(batch, all_reduce_max)
+        # One collective per step, of [scoring layers, tokens] (tests/test_selection.py:199-280).
+        assert calls == [(len(spec.scoring_layers), spec.total_tokens)]
         torch.cuda.synchronize()
         agg = pipeline.agg[: batch.total_tokens]
         if exact:
