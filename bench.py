@@ -67,6 +67,12 @@ def parse_args() -> argparse.Namespace:
         "compaction overwrites (outside the timed region; each step is timed with HIP events), so every "
         "step is a first compaction of the same cache instead of a re-compaction of its own output",
     )
+    p.add_argument(
+        "--score-aggregation",
+        choices=("mean", "max"),
+        default="mean",
+        help="aggregation of the rotary score over the future offsets (the reference's score_aggregation option)",
+    )
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument(
@@ -423,7 +429,7 @@ def stage_times(pipeline, batch, reps: int, restore=None) -> dict[str, float]:
     return {n: statistics.mean(m[i].elapsed_time(m[i + 1]) for m in marks) for i, n in enumerate(names)}
 
 
-def cpu_baseline(cache, spec, repeats: int) -> dict:
+def cpu_baseline(cache, spec, repeats: int, score_aggregation: str = "mean") -> dict:
     """Time the oracle (torch CPU restatement of the reference path) on one
     sequence: score the sampled layers, select, materialise every layer."""
     import torch
@@ -449,7 +455,7 @@ def cpu_baseline(cache, spec, repeats: int) -> dict:
     ]
     cfg = ref.MethodConfig(
         budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
-        score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
+        score_aggregation=score_aggregation, score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
     )
     offsets = ref.build_geometric_offsets(spec.max_model_len)
 
@@ -508,7 +514,7 @@ def main() -> int:
     spec = workloads.config_spec(args.config, **overrides)
     device = torch.device("cuda:0")
     cache = workloads.build_synthetic_cache(spec, device, seed=0, arena=args.arena)
-    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline, batch = workloads.build_pipeline(cache, score_aggregation=args.score_aggregation)
     torch.cuda.synchronize()
 
     restore = None
@@ -564,6 +570,7 @@ def main() -> int:
             + f", {cache.k_caches[0].shape[0]} pages each ({cache.k_caches[0].numel() * cache.k_caches[0].element_size() / 2**30:.2f} GiB)"
             + (", workload pages scattered through it" if spec.permute_pages else ""),
             "launch": "one HIP graph per step" if args.graph else "kernel launches per step",
+            **({"score_aggregation": "max"} if args.score_aggregation == "max" else {}),
             **(
                 {"timing": "sum of per-step HIP-event times; overwritten front pages restored before each step, untimed"}
                 if restore is not None
@@ -593,7 +600,7 @@ def main() -> int:
         "score_gbs": round(score_gbs, 1),
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cache, spec, args.cpu_repeats)
+        result["cpu_baseline"] = cpu_baseline(cache, spec, args.cpu_repeats, args.score_aggregation)
     print(json.dumps(result), flush=True)
     return 0
 

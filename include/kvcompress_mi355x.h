@@ -125,6 +125,46 @@ int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers, const uint64_t
                     int64_t raw_token_stride, int64_t raw_head_stride, void* workspace,
                     size_t workspace_bytes);
 
+/* Per-offset phase table for score_aggregation "max":
+ *   phase_cos[b][l][o][f] = cos((offsets[o] + round_starts[b]) * omega[l][f])
+ *   phase_sin[b][l][o][f] = sin((offsets[o] + round_starts[b]) * omega[l][f])
+ * with the argument formed in float32 as the torch path does and the cosine
+ * and sine rounded once from double.  Replaces the phases of the max branch of
+ * score_post_rope_keys (tri/scoring.py:77,84-91) for every sequence and
+ * scoring layer at once. */
+int kvc_offset_phases(kvc_stream_t stream, int n_seq, int n_layers, int n_freq,
+                      const int64_t* round_starts, const float* offsets, int n_offsets,
+                      const float* omega, float* phase_cos, float* phase_sin);
+
+/* Bytes of scratch kvc_score_paged_max needs for this shape and offset count
+ * (at least kvc_score_workspace_bytes of the same shape, so kvc_head_stats
+ * accepts the same workspace). 0 for an unsupported shape. */
+size_t kvc_score_max_workspace_bytes(int n_layers, int kv_heads, int head_dim, int rotary_dim,
+                                     int qpk, int n_seq, int max_seq_len, int n_offsets);
+
+/* Raw scores with the rotary term maximised over the future offsets instead of
+ * averaged: score_aggregation="max" of score_post_rope_keys
+ * (tri/scoring.py:84-97), which the reference runs through its torch fallback
+ * (tri/method.py:348-431):
+ *   score[l][b][t][h*qpk+g] = max_o sum_f a*((qr*kr+qi*ki)*cos_of - (qi*kr-qr*ki)*sin_of)
+ *                           + sum_f a*extra*|k_f| + sum_p q_pass*k_pass
+ * Arguments as kvc_score_paged except offset_cos/offset_sin: the
+ * kvc_offset_phases tables [n_seq][n_layers][n_offsets][F], sequence stride
+ * phase_seq_stride elements (0 = one table shared by all sequences).  Served
+ * for the matrix-core shapes only (bf16 or fp16, head_dim 64, 128 or 256,
+ * rotary_dim/2 a multiple of 32); KVC_EINVAL otherwise.  Partial sums for
+ * kvc_head_stats land where kvc_score_paged leaves them. */
+int kvc_score_paged_max(kvc_stream_t stream, int dtype, int n_layers, const uint64_t* k_layer_ptrs,
+                        int64_t num_pages, int64_t page_stride, int kv_heads, int head_dim,
+                        int rotary_dim, int qpk, int rope_style, int n_seq, int max_seq_len,
+                        const int32_t* seq_lens, const int64_t* token_offsets,
+                        const int64_t* block_offsets, const int64_t* block_ids, const float* q_real,
+                        const float* q_imag, const float* freq_scale, const float* extra_coef,
+                        const float* q_pass, const float* offset_cos, const float* offset_sin,
+                        int n_offsets, int64_t phase_seq_stride, float* raw,
+                        int64_t raw_layer_stride, int64_t raw_token_stride,
+                        int64_t raw_head_stride, void* workspace, size_t workspace_bytes);
+
 /* Population mean and variance of every query head's raw scores over the
  * sequence's tokens, from the partial sums kvc_score_paged left in the
  * workspace (torch.var_mean(raw, dim=-1, correction=0), tri/method.py:379-381,423).

@@ -25,16 +25,20 @@ def score_brute(
     rotary_dim: int | None = None,
     q_pass: np.ndarray | None = None,
     interleaved: bool = False,
+    aggregation: str = "mean",
 ) -> np.ndarray:
     """keys [T, kv, D]; stats [kv, qpk, F] (q_pass [kv, qpk, P]) -> [kv, qpk, T].
 
     The first term is the RoPE attention logit of the mean query rotated to
     the future position p = rs + o against the (already rotated) cached key:
-    Re( q_f e^{i p w_f} conj(k_f) ), averaged over the offsets o.
-    score = mean_o sum_f a_f Re( q_f e^{i (o+rs) w_f} conj(k_f) )
+    Re( q_f e^{i p w_f} conj(k_f) ), summed over frequencies and then averaged
+    (aggregation "mean") or maximised (aggregation "max") over the offsets o.
+    score = agg_o sum_f a_f Re( q_f e^{i (o+rs) w_f} conj(k_f) )
           + sum_f a_f (q_abs_f - |q_f|) |k_f|  + sum_p q_pass_p k_p
     with q_f = qr + i qi, k_f = kr + i ki, a_f = sqrt(freq_scale_sq).
     """
+    if aggregation not in ("mean", "max"):
+        raise ValueError(aggregation)
     keys = np.asarray(keys, dtype=np.float64)
     tokens, kv_heads, head_dim = keys.shape
     rotary = head_dim if rotary_dim is None else rotary_dim
@@ -45,6 +49,7 @@ def score_brute(
         for g in range(qpk):
             for t in range(tokens):
                 total = 0.0
+                per_offset = [0.0] * len(offsets)
                 for f in range(freq):
                     if interleaved:
                         kr, ki = keys[t, h, 2 * f], keys[t, h, 2 * f + 1]
@@ -54,12 +59,11 @@ def score_brute(
                     a = math.sqrt(float(freq_scale_sq[h, g, f]))
                     k = complex(kr, ki)
                     q = complex(qr, qi)
-                    acc = 0.0
-                    for o in offsets:
+                    for i, o in enumerate(offsets):
                         phi = (float(o) + round_start) * float(omega[f])
-                        acc += (q * complex(math.cos(phi), math.sin(phi)) * k.conjugate()).real
-                    total += a * acc / len(offsets)
+                        per_offset[i] += a * (q * complex(math.cos(phi), math.sin(phi)) * k.conjugate()).real
                     total += a * (float(q_abs[h, g, f]) - math.sqrt(qr * qr + qi * qi + 1e-8)) * abs(k)
+                total += sum(per_offset) / len(offsets) if aggregation == "mean" else max(per_offset)
                 if rotary < head_dim:
                     total += float(np.dot(np.asarray(q_pass[h, g], dtype=np.float64), keys[t, h, rotary:]))
                 out[h, g, t] = total

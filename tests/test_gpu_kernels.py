@@ -169,6 +169,73 @@ def test_score_paged_matches_oracle(hip_device, case) -> None:
     assert_scores_close(got[..., :tokens].reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
 
 
+MAX_CASES = [
+    # (kv, qpk, head_dim, rotary, style, dtype, tokens, max_model_len -> offsets)
+    (8, 5, 128, 128, "half", torch.bfloat16, 1000, 32768),        # 16 offsets, one chunk
+    (8, 5, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: two chunks, two head groups
+    (2, 4, 128, 128, "half", torch.bfloat16, 5000, 32768),        # several spans per workgroup
+    (2, 8, 256, 64, "half", torch.bfloat16, 700, 262144),         # partial RoPE, 19 offsets
+    (8, 5, 128, 128, "half", torch.float16, 513, 32768),
+    (8, 5, 128, 128, "interleaved", torch.bfloat16, 600, 131072),
+    (2, 8, 256, 64, "interleaved", torch.float16, 300, 32768),
+    (2, 4, 64, 64, "half", torch.bfloat16, 257, 8),               # 4 offsets
+    (1, 8, 256, 256, "half", torch.bfloat16, 130, 65536),         # F = 128: one query head per workgroup
+]
+
+
+@pytest.mark.parametrize("case", MAX_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5])[-4:]}t{c[6]}o{c[7]}" for c in MAX_CASES])
+def test_score_paged_max_matches_oracle(hip_device, case) -> None:
+    # score_aggregation="max" (tri/scoring.py:84-97) against the oracle's torch program.
+    kernels, _, _ = _kvc()
+    kv, qpk, head_dim, rotary, style, dtype, tokens, max_len = case
+    g = torch.Generator().manual_seed(sum(case[:4]) + tokens + max_len)
+    freq = rotary // 2
+    stats = _random_stats(g, kv, qpk, freq, head_dim - rotary, rotary, style=style)
+    n_blocks = -(-tokens // 128)
+    pool = n_blocks + 5
+    cache = torch.randn(pool, 128, kv, head_dim, generator=g).to(dtype)
+    blocks = torch.randperm(pool, generator=g)[:n_blocks]
+    offsets = ref.build_geometric_offsets(max_len)
+    round_start = tokens + 17
+    keys = ref.gather_paged_range(cache, blocks, start=0, count=tokens, block_size=128)
+    want = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets, aggregation="max")
+    out = torch.full((kv, qpk, tokens + 3), float("nan"), device=hip_device)
+    d = lambda t: None if t is None else t.to(hip_device)  # noqa: E731
+    assert kernels.score_paged_keys_max(
+        cache.to(hip_device), blocks.to(hip_device), d(stats.q_mean_real), d(stats.q_mean_imag),
+        d(torch.sqrt(stats.freq_scale_sq)),
+        d(stats.q_abs_mean - torch.sqrt(stats.q_mean_real.square() + stats.q_mean_imag.square() + 1e-8)),
+        d(stats.omega), d(offsets), round_start, tokens, out, 128, style,
+        q_pass_mean=d(stats.q_pass_mean), rotary_dim=rotary if rotary != head_dim else None,
+    )
+    got = out.cpu()
+    assert torch.isnan(got[..., tokens:]).all(), "scorer wrote past num_tokens"
+    assert_scores_close(got[..., :tokens].reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
+    # The maximum is not the mean: the two aggregations differ on these inputs.
+    mean = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets)
+    assert float((want - mean).abs().max()) > 1e-2
+
+
+def test_offset_phase_table_matches_torch(hip_device) -> None:
+    from kvcompress_mi355x import _native
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    offsets = ref.build_geometric_offsets(131072)
+    omega = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    omega2 = torch.stack([omega, omega * 0.5]).to(hip_device)
+    rs = torch.tensor([300, 131072], dtype=torch.int64, device=hip_device)
+    n_off, freq = offsets.numel(), omega.numel()
+    cos = torch.empty(2, 2, n_off, freq, device=hip_device)
+    sin = torch.empty_like(cos)
+    _native.call("kvc_offset_phases", dev.stream_handle(cos.device), 2, 2, freq, dev.ptr(rs), dev.ptr(offsets.to(hip_device)),
+                 n_off, dev.ptr(omega2), dev.ptr(cos), dev.ptr(sin))
+    for b in range(2):
+        for layer in range(2):
+            phases = (offsets.unsqueeze(1) + float(rs[b])) * omega2[layer].cpu().unsqueeze(0)
+            torch.testing.assert_close(cos[b, layer].cpu(), torch.cos(phases), rtol=0, atol=2e-6)
+            torch.testing.assert_close(sin[b, layer].cpu(), torch.sin(phases), rtol=0, atol=2e-6)
+
+
 def test_reference_smoke_inputs_with_shifted_phases(hip_device) -> None:
     # The reference device smoke (tests/run_npu_kernel_smoke.py:83-138) widened to
     # a 16-dim head: linspace keys and statistics, angle-addition phases at

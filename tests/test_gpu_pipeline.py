@@ -18,11 +18,12 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
-def _oracle_for(host, spec, b):
+def _oracle_for(host, spec, b, score_aggregation="mean", layer_aggregation="mean"):
     stats = host.calibration.to_device(spec.model_shape(), torch.device("cpu"))
     layer_stats = [oracle_stats(stats[layer]) for layer in spec.scoring_layers]
     cfg = ref.MethodConfig(
         budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
+        score_aggregation=score_aggregation, layer_aggregation=layer_aggregation,
         score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
     )
     return ref.method_select(
@@ -46,12 +47,14 @@ def _protected(n, spec):
     return mask
 
 
-def _run_and_check(spec, hip_device, *, check_layers=None):
+def _run_and_check(spec, hip_device, *, check_layers=None, score_aggregation="mean", layer_aggregation="mean"):
     from kvcompress_mi355x import workloads
 
     host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
     cache = workloads.move_cache(host, hip_device)
-    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline, batch = workloads.build_pipeline(
+        cache, score_aggregation=score_aggregation, layer_aggregation=layer_aggregation
+    )
     keep, tables, freed = pipeline.step(batch)
     torch.cuda.synchronize()
     offs = [0]
@@ -62,7 +65,7 @@ def _run_and_check(spec, hip_device, *, check_layers=None):
     oracle_keeps = []
     head_mean, head_var = pipeline.head_statistics(batch)
     for b, n in enumerate(spec.seq_lens):
-        out = _oracle_for(host, spec, b)
+        out = _oracle_for(host, spec, b, score_aggregation, layer_aggregation)
         for s_idx in range(len(spec.scoring_layers)):
             got_raw = pipeline.raw_scores()[s_idx, offs[b] : offs[b + 1], :h_q].t()
             assert_scores_close(got_raw, out["raw"][s_idx].reshape(h_q, n))
@@ -129,6 +132,27 @@ def test_inplace_front_pages_with_outliers(hip_device) -> None:
 
     spec = workloads.config_spec(4, n_layers=2, score_layer_stride=1, seq_lens=(12000, 20000), pool_pages=300, max_model_len=32768)
     _run_and_check(spec, hip_device)
+
+
+@pytest.mark.parametrize(
+    "config, overrides, layer_aggregation",
+    [
+        # 18 offsets: two 16-offset chunks, query heads split over two workgroups.
+        (2, dict(n_layers=4, score_layer_stride=2, seq_lens=(5000, 8192), budget=4096, max_model_len=131072), "max"),
+        # Partial RoPE (F = 32), 19 offsets, v3 selection.
+        (3, dict(n_layers=4, seq_lens=(9000, 6000)), "mean"),
+        # fp16 keys, 16 offsets.
+        (5, dict(n_layers=2, score_layer_stride=1, seq_lens=(4300, 7000)), "mean"),
+    ],
+    ids=["qwen2.5-14b-o18-layer-max", "qwen3.5-o19", "fp16-o16"],
+)
+def test_score_aggregation_max(hip_device, config, overrides, layer_aggregation) -> None:
+    # score_aggregation="max" (tri/scoring.py:84-97) through the batched step.
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(config, **overrides)
+    _, _, _, near = _run_and_check(spec, hip_device, score_aggregation="max", layer_aggregation=layer_aggregation)
+    assert near <= 4
 
 
 def test_fp16_decode_shape(hip_device) -> None:

@@ -144,6 +144,62 @@ def test_oracle_matches_float64_brute_force(head_dim: int, rotary: int, style: s
     assert np.max(np.abs(got - expected)) <= tol * scale
 
 
+@pytest.mark.parametrize(
+    ("head_dim", "rotary", "style", "n_offsets"),
+    [(16, 16, "half", 16), (16, 16, "interleaved", 18), (32, 16, "half", 5), (48, 32, "interleaved", 19)],
+)
+def test_oracle_max_matches_float64_brute_force(head_dim: int, rotary: int, style: str, n_offsets: int) -> None:
+    # tri/scoring.py:84-97: the rotary sum is maximised over the offsets, then
+    # the magnitude and pass terms are added.
+    g = torch.Generator().manual_seed(7 * head_dim + n_offsets)
+    kv, qpk, tokens, rs = 2, 3, 6, 300
+    freq = rotary // 2
+    qr, qi = torch.randn(kv, qpk, freq, generator=g), torch.randn(kv, qpk, freq, generator=g)
+    qa = torch.sqrt(qr.square() + qi.square()) + torch.rand(kv, qpk, freq, generator=g)
+    fs = torch.rand(kv, qpk, freq, generator=g) + 0.5
+    omega = 1.0 / (1e4 ** (torch.arange(0, rotary, 2, dtype=torch.float32) / rotary))
+    qp = torch.randn(kv, qpk, head_dim - rotary, generator=g) if head_dim > rotary else None
+    keys = torch.randn(tokens, kv, head_dim, generator=g).to(torch.bfloat16)
+    stats = ref.LayerStats(qr, qi, qa, fs, omega, style, rotary, qp)
+    offsets = ref.build_geometric_offsets(2 ** (n_offsets - 1))
+    assert offsets.numel() == n_offsets
+    got = ref.score_post_rope_keys(keys, stats, round_start=rs, offsets=offsets, aggregation="max").double().numpy()
+    args = (keys.float().numpy(), qr.numpy(), qi.numpy(), qa.numpy(), fs.numpy(), omega.numpy(), [float(o) for o in offsets], rs)
+    kw = dict(rotary_dim=rotary, q_pass=None if qp is None else qp.numpy(), interleaved=style == "interleaved")
+    expected = brute.score_brute(*args, aggregation="max", **kw)
+    scale = np.abs(expected).max() + 1.0
+    assert np.max(np.abs(got - expected)) <= 2e-3 * scale
+    # The maximum over offsets is at least their mean, and strictly above it
+    # somewhere for random phases.
+    mean = brute.score_brute(*args, aggregation="mean", **kw)
+    assert np.all(expected >= mean - 1e-9) and np.any(expected > mean + 1e-3)
+
+
+def test_max_aggregation_reduces_to_mean() -> None:
+    # One offset, or omega = 0 (every offset has phase 0): max over offsets = mean.
+    g = torch.Generator().manual_seed(12)
+    kv, qpk, freq = 1, 2, 8
+    qr, qi = torch.randn(kv, qpk, freq, generator=g), torch.randn(kv, qpk, freq, generator=g)
+    qa = torch.sqrt(qr.square() + qi.square()) + 0.25
+    fs = torch.rand(kv, qpk, freq, generator=g) + 0.5
+    keys = torch.randn(9, kv, 2 * freq, generator=g)
+    omega = 1.0 / (1e6 ** (torch.arange(0, 2 * freq, 2, dtype=torch.float32) / (2 * freq)))
+    one = torch.tensor([64.0])
+    stats = ref.LayerStats(qr, qi, qa, fs, omega)
+    torch.testing.assert_close(
+        ref.score_post_rope_keys(keys, stats, round_start=999, offsets=one, aggregation="max"),
+        ref.score_post_rope_keys(keys, stats, round_start=999, offsets=one, aggregation="mean"),
+        rtol=1e-6, atol=1e-6,
+    )
+    flat = ref.LayerStats(qr, qi, qa, fs, torch.zeros(freq))
+    offs = ref.build_geometric_offsets(1 << 17)
+    torch.testing.assert_close(
+        ref.score_post_rope_keys(keys, flat, round_start=5, offsets=offs, aggregation="max"),
+        ref.score_post_rope_keys(keys, flat, round_start=5, offsets=offs, aggregation="mean"),
+        rtol=1e-5, atol=1e-5,
+    )
+
+
 def test_oracle_phase_arguments_match_float32_brute_force() -> None:
     # Evaluating the brute force at the float32-rounded phase argument removes
     # the argument rounding: then agreement is to float32 arithmetic precision.

@@ -65,6 +65,28 @@ __global__ void mean_phases_kernel(int n_seq, int n_layers, int n_freq,
   phase_sin[idx] = __fdiv_rn(s, n);
 }
 
+// One thread per (sequence, layer, offset, frequency): cos and sin of the
+// float32 phase argument (offset + round_start) * omega, as the torch path
+// forms it, evaluated in double and rounded once.  Layout [b][l][o][f].
+__global__ void offset_phases_kernel(int n_seq, int n_layers, int n_freq, const int64_t* __restrict__ round_starts,
+                                     const float* __restrict__ offsets, int n_offsets, const float* __restrict__ omega,
+                                     float* __restrict__ phase_cos, float* __restrict__ phase_sin) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t per_layer = static_cast<int64_t>(n_offsets) * n_freq;
+  const int64_t per_seq = per_layer * n_layers;
+  if (idx >= per_seq * n_seq) return;
+  const int64_t b = idx / per_seq;
+  const int64_t r = idx - b * per_seq;
+  const int64_t l = r / per_layer;
+  const int64_t of = r - l * per_layer;
+  const int o = static_cast<int>(of / n_freq);
+  const int f = static_cast<int>(of - static_cast<int64_t>(o) * n_freq);
+  const float rs = static_cast<float>(round_starts[b]);
+  const float x = __fmul_rn(__fadd_rn(offsets[o], rs), omega[l * n_freq + f]);
+  phase_cos[idx] = static_cast<float>(cos(static_cast<double>(x)));
+  phase_sin[idx] = static_cast<float>(sin(static_cast<double>(x)));
+}
+
 // Angle addition from precomputed offset means (tri/kernels.py:70-82).
 __global__ void shift_phases_kernel(int n_values, float round_start,
                                     const float* __restrict__ omega,
@@ -598,6 +620,19 @@ extern "C" int kvc_mean_phases(kvc_stream_t stream, int n_seq, int n_layers, int
   return launch_status("kvc_mean_phases");
 }
 
+extern "C" int kvc_offset_phases(kvc_stream_t stream, int n_seq, int n_layers, int n_freq,
+                                 const int64_t* round_starts, const float* offsets, int n_offsets,
+                                 const float* omega, float* phase_cos, float* phase_sin) {
+  if (n_seq <= 0 || n_layers <= 0 || n_freq <= 0 || n_offsets <= 0)
+    return fail(KVC_EINVAL, "kvc_offset_phases: sizes must be positive");
+  if (!round_starts || !offsets || !omega || !phase_cos || !phase_sin)
+    return fail(KVC_EINVAL, "kvc_offset_phases: null pointer");
+  const int64_t total = static_cast<int64_t>(n_seq) * n_layers * n_offsets * n_freq;
+  offset_phases_kernel<<<static_cast<unsigned>(ceil_div(total, 256)), 256, 0, as_stream(stream)>>>(
+      n_seq, n_layers, n_freq, round_starts, offsets, n_offsets, omega, phase_cos, phase_sin);
+  return launch_status("kvc_offset_phases");
+}
+
 extern "C" int kvc_shift_mean_phases(kvc_stream_t stream, int n_values, int64_t round_start,
                                      const float* omega, const float* offset_cos_mean,
                                      const float* offset_sin_mean, float* phase_cos,
@@ -631,6 +666,90 @@ extern "C" int kvc_score_raw_layout(int dtype, int rope_style, int kv_heads, int
   return mfma_scorer_supported(s, dtype, rope_style) ? KVC_RAW_HEAD_MAJOR : KVC_RAW_TOKEN_MAJOR;
 }
 
+namespace kvc {
+namespace {
+
+// Checks and argument blocks shared by kvc_score_paged and kvc_score_paged_max.
+// `phase_bytes_ok` is false when the caller's phase tables cannot be read by
+// this entry (checked by the caller).  Returns 0 or a C-ABI error code.
+int score_setup(const char* who, int dtype, int n_layers, const uint64_t* k_layer_ptrs, int64_t num_pages,
+                int64_t page_stride, int kv_heads, int head_dim, int rotary_dim, int qpk, int rope_style, int n_seq,
+                int max_seq_len, const int32_t* seq_lens, const int64_t* token_offsets, const int64_t* block_offsets,
+                const int64_t* block_ids, const float* q_real, const float* q_imag, const float* freq_scale,
+                const float* extra_coef, const float* q_pass, const float* phase_cos, const float* phase_sin,
+                int64_t phase_seq_stride, float* raw, int64_t raw_layer_stride, int64_t raw_token_stride,
+                int64_t raw_head_stride, void* workspace, size_t workspace_bytes_given, size_t workspace_needed,
+                ScoreShape* s, FoldArgs* fa, ScoreArgs* sa) {
+  if (!make_shape(s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len))
+    return fail(KVC_EINVAL,
+                "%s: unsupported shape (layers=%d kv_heads=%d head_dim=%d "
+                "rotary_dim=%d qpk=%d n_seq=%d); rotary_dim and head_dim-rotary_dim must be "
+                "multiples of 16, qpk <= 8",
+                who, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq);
+  if (dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16)
+    return fail(KVC_EINVAL, "%s: dtype must be bf16 or fp16", who);
+  if (rope_style != KVC_ROPE_HALF && rope_style != KVC_ROPE_INTERLEAVED)
+    return fail(KVC_EINVAL, "%s: unknown rope style %d", who, rope_style);
+  if (page_stride < static_cast<int64_t>(kBlockSize) * kv_heads * head_dim || num_pages <= 0)
+    return fail(KVC_EINVAL, "%s: page stride smaller than a page", who);
+  if (!k_layer_ptrs || !seq_lens || !token_offsets || !block_offsets || !block_ids || !q_real ||
+      !q_imag || !freq_scale || !extra_coef || !phase_cos || !phase_sin || !raw || !workspace)
+    return fail(KVC_EINVAL, "%s: null pointer", who);
+  if (s->pass > 0 && !q_pass)
+    return fail(KVC_EINVAL, "%s: partial RoPE requires q_pass", who);
+  if (workspace_bytes_given < workspace_needed)
+    return fail(KVC_EINVAL, "%s: workspace too small (%zu < %zu)", who, workspace_bytes_given, workspace_needed);
+
+  fa->n_seq = n_seq;
+  fa->n_layers = n_layers;
+  fa->kv_heads = kv_heads;
+  fa->qpk = qpk;
+  fa->freq = s->freq;
+  fa->pass = s->pass;
+  fa->units_rot = s->units_rot;
+  fa->units = s->units;
+  fa->rotary_dim = rotary_dim;
+  fa->interleaved = rope_style == KVC_ROPE_INTERLEAVED ? 1 : 0;
+  fa->zero_rotary = 0;
+  fa->q_real = q_real;
+  fa->q_imag = q_imag;
+  fa->scale = freq_scale;
+  fa->extra = extra_coef;
+  fa->q_pass = q_pass;
+  fa->phase_cos = phase_cos;
+  fa->phase_sin = phase_sin;
+  fa->phase_seq_stride = phase_seq_stride;
+  fa->weights = static_cast<float*>(workspace);
+
+  sa->k_layer_ptrs = k_layer_ptrs;
+  sa->num_pages = num_pages;
+  sa->page_stride = page_stride;
+  sa->kv_heads = kv_heads;
+  sa->head_dim = head_dim;
+  sa->rotary_dim = rotary_dim;
+  sa->freq = s->freq;
+  sa->units_rot = s->units_rot;
+  sa->units = s->units;
+  sa->group_shift = s->group_shift;
+  sa->n_seq = n_seq;
+  sa->max_tiles = s->max_tiles;
+  sa->n_layers = n_layers;
+  sa->seq_lens = seq_lens;
+  sa->token_offsets = token_offsets;
+  sa->block_offsets = block_offsets;
+  sa->block_ids = block_ids;
+  sa->weights = static_cast<float*>(workspace);
+  sa->raw = raw;
+  sa->raw_layer_stride = raw_layer_stride;
+  sa->raw_token_stride = raw_token_stride;
+  sa->raw_head_stride = raw_head_stride;
+  sa->partials = reinterpret_cast<double*>(static_cast<char*>(workspace) + weights_bytes_aligned(*s));
+  return 0;
+}
+
+}  // namespace
+}  // namespace kvc
+
 extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
                                const uint64_t* k_layer_ptrs, int64_t num_pages,
                                int64_t page_stride, int kv_heads, int head_dim, int rotary_dim,
@@ -644,78 +763,19 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
                                int64_t raw_token_stride, int64_t raw_head_stride, void* workspace,
                                size_t workspace_bytes_given) {
   ScoreShape s;
-  if (!make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len))
-    return fail(KVC_EINVAL,
-                "kvc_score_paged: unsupported shape (layers=%d kv_heads=%d head_dim=%d "
-                "rotary_dim=%d qpk=%d n_seq=%d); rotary_dim and head_dim-rotary_dim must be "
-                "multiples of 16, qpk <= 8",
-                n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq);
-  if (dtype != KVC_DTYPE_BF16 && dtype != KVC_DTYPE_FP16)
-    return fail(KVC_EINVAL, "kvc_score_paged: dtype must be bf16 or fp16");
-  if (rope_style != KVC_ROPE_HALF && rope_style != KVC_ROPE_INTERLEAVED)
-    return fail(KVC_EINVAL, "kvc_score_paged: unknown rope style %d", rope_style);
-  if (page_stride < static_cast<int64_t>(kBlockSize) * kv_heads * head_dim || num_pages <= 0)
-    return fail(KVC_EINVAL, "kvc_score_paged: page stride smaller than a page");
-  if (!k_layer_ptrs || !seq_lens || !token_offsets || !block_offsets || !block_ids || !q_real ||
-      !q_imag || !freq_scale || !extra_coef || !phase_cos || !phase_sin || !raw || !workspace)
-    return fail(KVC_EINVAL, "kvc_score_paged: null pointer");
-  if (s.pass > 0 && !q_pass)
-    return fail(KVC_EINVAL, "kvc_score_paged: partial RoPE requires q_pass");
-  if (workspace_bytes_given < workspace_bytes(s))
-    return fail(KVC_EINVAL, "kvc_score_paged: workspace too small (%zu < %zu)",
-                workspace_bytes_given, workspace_bytes(s));
+  FoldArgs fa;
+  ScoreArgs sa;
+  const size_t need = make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len)
+                          ? workspace_bytes(s)
+                          : 0;
+  if (int rc = score_setup("kvc_score_paged", dtype, n_layers, k_layer_ptrs, num_pages, page_stride, kv_heads,
+                           head_dim, rotary_dim, qpk, rope_style, n_seq, max_seq_len, seq_lens, token_offsets,
+                           block_offsets, block_ids, q_real, q_imag, freq_scale, extra_coef, q_pass, phase_cos,
+                           phase_sin, phase_seq_stride, raw, raw_layer_stride, raw_token_stride, raw_head_stride,
+                           workspace, workspace_bytes_given, need, &s, &fa, &sa))
+    return rc;
   if (s.max_tiles == 0) return 0;
   hipStream_t st = as_stream(stream);
-
-  float* weights = static_cast<float*>(workspace);
-  double* partials =
-      reinterpret_cast<double*>(static_cast<char*>(workspace) + weights_bytes_aligned(s));
-
-  FoldArgs fa;
-  fa.n_seq = n_seq;
-  fa.n_layers = n_layers;
-  fa.kv_heads = kv_heads;
-  fa.qpk = qpk;
-  fa.freq = s.freq;
-  fa.pass = s.pass;
-  fa.units_rot = s.units_rot;
-  fa.units = s.units;
-  fa.rotary_dim = rotary_dim;
-  fa.interleaved = rope_style == KVC_ROPE_INTERLEAVED ? 1 : 0;
-  fa.q_real = q_real;
-  fa.q_imag = q_imag;
-  fa.scale = freq_scale;
-  fa.extra = extra_coef;
-  fa.q_pass = q_pass;
-  fa.phase_cos = phase_cos;
-  fa.phase_sin = phase_sin;
-  fa.phase_seq_stride = phase_seq_stride;
-  fa.weights = weights;
-
-  ScoreArgs sa;
-  sa.k_layer_ptrs = k_layer_ptrs;
-  sa.num_pages = num_pages;
-  sa.page_stride = page_stride;
-  sa.kv_heads = kv_heads;
-  sa.head_dim = head_dim;
-  sa.rotary_dim = rotary_dim;
-  sa.freq = s.freq;
-  sa.units_rot = s.units_rot;
-  sa.units = s.units;
-  sa.group_shift = s.group_shift;
-  sa.n_seq = n_seq;
-  sa.max_tiles = s.max_tiles;
-  sa.n_layers = n_layers;
-  sa.seq_lens = seq_lens;
-  sa.token_offsets = token_offsets;
-  sa.block_offsets = block_offsets;
-  sa.block_ids = block_ids;
-  sa.weights = weights;
-  sa.raw = raw;
-  sa.raw_layer_stride = raw_layer_stride;
-  sa.raw_token_stride = raw_token_stride;
-  sa.raw_head_stride = raw_head_stride;
-  sa.partials = partials;
 
   if (mfma_scorer_supported(s, dtype, rope_style)) return launch_mfma_scorer(st, s, dtype, fa, sa, workspace);
 
@@ -737,6 +797,48 @@ extern "C" int kvc_score_paged(kvc_stream_t stream, int dtype, int n_layers,
     return fail(KVC_EINVAL, "kvc_score_paged: too many sequences or layers for one launch");
   kern<<<grid, kScoreThreads, 0, st>>>(sa);
   return launch_status("kvc_score_paged");
+}
+
+extern "C" size_t kvc_score_max_workspace_bytes(int n_layers, int kv_heads, int head_dim, int rotary_dim, int qpk,
+                                                int n_seq, int max_seq_len, int n_offsets) {
+  ScoreShape s;
+  if (n_offsets <= 0 || !make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len)) return 0;
+  return max_workspace_bytes(s, n_offsets);
+}
+
+extern "C" int kvc_score_paged_max(kvc_stream_t stream, int dtype, int n_layers, const uint64_t* k_layer_ptrs,
+                                   int64_t num_pages, int64_t page_stride, int kv_heads, int head_dim,
+                                   int rotary_dim, int qpk, int rope_style, int n_seq, int max_seq_len,
+                                   const int32_t* seq_lens, const int64_t* token_offsets,
+                                   const int64_t* block_offsets, const int64_t* block_ids, const float* q_real,
+                                   const float* q_imag, const float* freq_scale, const float* extra_coef,
+                                   const float* q_pass, const float* offset_cos, const float* offset_sin,
+                                   int n_offsets, int64_t phase_seq_stride, float* raw, int64_t raw_layer_stride,
+                                   int64_t raw_token_stride, int64_t raw_head_stride, void* workspace,
+                                   size_t workspace_bytes_given) {
+  ScoreShape s;
+  FoldArgs fa;
+  ScoreArgs sa;
+  if (n_offsets <= 0) return fail(KVC_EINVAL, "kvc_score_paged_max: n_offsets must be positive");
+  const size_t need = make_shape(&s, n_layers, kv_heads, head_dim, rotary_dim, qpk, n_seq, max_seq_len)
+                          ? max_workspace_bytes(s, n_offsets)
+                          : 0;
+  if (int rc = score_setup("kvc_score_paged_max", dtype, n_layers, k_layer_ptrs, num_pages, page_stride, kv_heads,
+                           head_dim, rotary_dim, qpk, rope_style, n_seq, max_seq_len, seq_lens, token_offsets,
+                           block_offsets, block_ids, q_real, q_imag, freq_scale, extra_coef, q_pass, offset_cos,
+                           offset_sin, phase_seq_stride, raw, raw_layer_stride, raw_token_stride, raw_head_stride,
+                           workspace, workspace_bytes_given, need, &s, &fa, &sa))
+    return rc;
+  if (!mfma_scorer_supported(s, dtype, rope_style))
+    return fail(KVC_EINVAL,
+                "kvc_score_paged_max: the max-over-offsets scorer needs the matrix-core shape "
+                "(head_dim 64, 128 or 256 and rotary_dim/2 a multiple of 32)");
+  if (phase_seq_stride != 0 && phase_seq_stride < static_cast<int64_t>(n_layers) * n_offsets * s.freq)
+    return fail(KVC_EINVAL, "kvc_score_paged_max: phase_seq_stride smaller than one sequence's table");
+  if (s.max_tiles == 0) return 0;
+  if (n_seq > 65535 || n_layers > 65535)
+    return fail(KVC_EINVAL, "kvc_score_paged_max: too many sequences or layers for one launch");
+  return launch_max_scorer(as_stream(stream), s, dtype, n_offsets, fa, sa, workspace);
 }
 
 extern "C" int kvc_head_stats(kvc_stream_t stream, int n_layers, int kv_heads, int head_dim,

@@ -118,10 +118,27 @@ inline size_t partial_count(const ScoreShape& s) {
 inline size_t workspace_bytes(const ScoreShape& s) {
   return weights_bytes_aligned(s) + partial_count(s) * 2 * sizeof(double);
 }
+// Max-over-offsets scorer: after the mean scorer's workspace (whose weight
+// region holds the magnitude and pass fragments and whose partial sums feed
+// kvc_head_stats unchanged), the per-offset rotary fragments
+// [n_seq][n_layers][kv_heads][qpk][chunk][step][hi/lo][64 lanes] of 16 bytes,
+// chunk = 16 offsets and step = 32 rotary dims, then one float column scale
+// per (sequence, layer, KV head, query head).
+inline int offset_chunks(int n_offsets) { return (n_offsets + 15) / 16; }
+inline size_t offset_fragment_bytes(const ScoreShape& s, int n_offsets) {
+  return static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk * offset_chunks(n_offsets) * (s.freq / 16) *
+         2 * 64 * 16;
+}
+inline size_t max_tail_offset(const ScoreShape& s) { return (workspace_bytes(s) + 255) / 256 * 256; }
+inline size_t max_workspace_bytes(const ScoreShape& s, int n_offsets) {
+  const size_t frag = (offset_fragment_bytes(s, n_offsets) + 255) / 256 * 256;
+  return max_tail_offset(s) + frag + static_cast<size_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk * sizeof(float);
+}
 
 
 struct FoldArgs {
   int n_seq, n_layers, kv_heads, qpk, freq, pass, units_rot, units, rotary_dim, interleaved;
+  int zero_rotary;  // 1: rotary linear weights are 0 (the max scorer adds its own rotary term)
   const float* q_real;
   const float* q_imag;
   const float* scale;
@@ -154,5 +171,13 @@ struct ScoreArgs {
 bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style);
 int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, const ScoreArgs& sa,
                        void* weights);
+// Max-over-offsets scorer (score_max.hip): fold of the per-offset fragments,
+// magnitude/pass fold (zero_rotary) and scoring.  `fa.phase_cos/phase_sin`
+// are the per-offset tables [n_seq][n_layers][n_offsets][F].
+int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_offsets, const FoldArgs& fa,
+                      const ScoreArgs& sa, void* workspace);
+// The weight fold alone: bf16 or fp16 hi/lo fragments (and fp16 column scales)
+// into `weights`, laid out as the MFMA scorer reads them.
+int launch_mfma_fold(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, void* weights);
 
 }  // namespace kvc

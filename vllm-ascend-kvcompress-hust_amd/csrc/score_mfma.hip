@@ -40,7 +40,7 @@
 // float64 per-tile partial sums have the same layout as the VALU scorer's, so
 // kvc_head_stats and kvc_aggregate are shared.
 
-#include "score_internal.h"
+#include "mfma_common.h"
 
 #ifndef KVC_MFMA_GROUP
 #define KVC_MFMA_GROUP 2  // 16-token tiles per prefetch group
@@ -49,71 +49,7 @@
 namespace kvc {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Two floats -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-}
-// Two floats -> packed fp16 pair, round to nearest even (one v_cvt_pk_f16_f32).
-__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
-}
-
-// The 16-bit element type of a cache: A/B operand vector, the MFMA, the
-// unpacking and hi/lo packing of |k|.
-template <bool F16>
-struct MfmaElem;
-template <>
-struct MfmaElem<false> {
-  typedef bf16x8 vec;
-  static constexpr float kMagScale = 1.0f;
-  __device__ __forceinline__ static f32x4 mfma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static float lo(uint32_t w) { return bf16_lo(w); }
-  __device__ __forceinline__ static float hi(uint32_t w) { return bf16_hi(w); }
-  __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_bf16(a, b); }
-};
-template <>
-struct MfmaElem<true> {
-  typedef f16x8 vec;
-  static constexpr float kMagScale = 0.25f;  // |k| of fp16 keys reaches 2^16.5
-  __device__ __forceinline__ static f32x4 mfma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static float lo(uint32_t w) { return fp16_lo(w); }
-  __device__ __forceinline__ static float hi(uint32_t w) { return fp16_hi(w); }
-  __device__ __forceinline__ static uint32_t pack(float a, float b) { return pack_f16(a, b); }
-};
-
-// K is read once per scoring layer.  Non-temporal loads (meant to keep K from
-// evicting the weight fragments in L2) measured 0.85 ms against 0.72 ms for
-// plain loads on the Qwen2.5-14B shape, so they are off by default.
-#ifndef KVC_SCORE_NT_K
-#define KVC_SCORE_NT_K 0
-#endif
-__device__ __forceinline__ u32x4 load_k(KVC_GLOBAL const u32x4* p) {
-  if (KVC_SCORE_NT_K) return __builtin_nontemporal_load(p);
-  return *p;
-}
-
-// Round-to-nearest-even float32 -> bf16 bits (finite inputs).
-__device__ __forceinline__ uint32_t bf16_bits(float x) {
-  const uint32_t u = __float_as_uint(x);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-__device__ __forceinline__ float bf16_value(uint32_t bits) { return __uint_as_float(bits << 16); }
-
 constexpr int kMfmaMaxHeadsPerWg = 4;            // hpw
-constexpr int kMfmaMaxQpk = 8;                   // make_shape admits qpk <= 8
-constexpr int kStageStride = kScoreTile + 4;     // floats per staged query-head row
 
 struct MfmaGeometry {
   int nk, nf;         // linear / magnitude K steps of 32
@@ -153,6 +89,7 @@ __device__ __forceinline__ float folded_weight(const FoldArgs& a, int nk, int b,
     const int d = 32 * step + 8 * kb + e;
     if (d >= head_dim) return 0.0f;
     if (d < 2 * a.freq) {
+      if (a.zero_rotary) return 0.0f;
       const float* pc = a.phase_cos + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
       const float* ps = a.phase_sin + b * a.phase_seq_stride + static_cast<int64_t>(layer) * a.freq;
       // Half style: real parts in dims [0, F), imaginary in [F, 2F); interleaved: (2f, 2f+1).
@@ -375,32 +312,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     }
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
-      u32x4 hi, lo;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        // Two frequencies per output word: half style pairs word w of steps q
-        // (real) and q+NF (imaginary); interleaved takes words 2w, 2w+1 of
-        // step 2q (w < 2) or 2q+1, each word one (real, imaginary) pair.
-        uint32_t re_w, im_w;
-        if (IL) {
-          const uint32_t w0 = ka[2 * q + (w >> 1)][(2 * w) & 3], w1 = ka[2 * q + (w >> 1)][(2 * w + 1) & 3];
-          // (re0, re1) = (lo of w0, lo of w1), (im0, im1) = (hi of w0, hi of w1)
-          re_w = (w0 & 0xffffu) | (w1 << 16);
-          im_w = (w0 >> 16) | (w1 & 0xffff0000u);
-        } else {
-          re_w = ka[q][w];
-          im_w = ka[q + NF][w];
-        }
-        const float re0 = E::lo(re_w), re1 = E::hi(re_w);
-        const float im0 = E::lo(im_w), im1 = E::hi(im_w);
-        const float m0 = __builtin_amdgcn_sqrtf(fmaf(im0, im0, re0 * re0)) * E::kMagScale;
-        const float m1 = __builtin_amdgcn_sqrtf(fmaf(im1, im1, re1 * re1)) * E::kMagScale;
-        const uint32_t h = E::pack(m0, m1);
-        hi[w] = h;
-        lo[w] = E::pack(m0 - E::lo(h), m1 - E::hi(h));
-      }
-      const vec_t khi = __builtin_bit_cast(vec_t, hi);
-      const vec_t klo = __builtin_bit_cast(vec_t, lo);
+      vec_t khi, klo;
+      magnitude_operands<F16, IL, NK, NF>(ka, q, &khi, &klo);
       acc0 = E::mfma(khi, m_hi[q], acc0);
       acc1 = E::mfma(khi, m_lo[q], acc1);
       acc0 = E::mfma(klo, m_hi[q], acc0);
@@ -529,11 +442,8 @@ bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style) {
   return pick(s.head_dim / 32, s.freq / 32, dtype, rope_style) != nullptr;
 }
 
-int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, const ScoreArgs& sa,
-                       void* weights) {
+int launch_mfma_fold(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, void* weights) {
   const MfmaGeometry geo = geometry(s);
-  MfmaKernel kern = pick(geo.nk, geo.nf, dtype, fa.interleaved ? KVC_ROPE_INTERLEAVED : KVC_ROPE_HALF);
-  if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: no MFMA scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
   uint16_t* frags = static_cast<uint16_t*>(weights);
   float* inv_scale = reinterpret_cast<float*>(static_cast<char*>(weights) + mfma_fragment_only_bytes(s));
   if (dtype == KVC_DTYPE_FP16) {
@@ -543,7 +453,17 @@ int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const
     const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * (2 * geo.nk + 2 * geo.nf) * 4 * s.qpk;
     fold_mfma_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 256)), 256, 0, stream>>>(fa, geo.nk, geo.nf, frags);
   }
-  if (int rc = launch_status("kvc_score_paged(fold)")) return rc;
+  return launch_status("kvc_score_paged(fold)");
+}
+
+int launch_mfma_scorer(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, const ScoreArgs& sa,
+                       void* weights) {
+  const MfmaGeometry geo = geometry(s);
+  MfmaKernel kern = pick(geo.nk, geo.nf, dtype, fa.interleaved ? KVC_ROPE_INTERLEAVED : KVC_ROPE_HALF);
+  if (!kern) return fail(KVC_EINVAL, "kvc_score_paged: no MFMA scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
+  if (int rc = launch_mfma_fold(stream, s, dtype, fa, weights)) return rc;
+  const uint16_t* frags = static_cast<const uint16_t*>(weights);
+  const float* inv_scale = reinterpret_cast<const float*>(static_cast<const char*>(weights) + mfma_fragment_only_bytes(s));
   const int64_t gx = static_cast<int64_t>(s.max_tiles) * geo.head_groups;
   if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_score_paged: grid too large");
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(s.n_seq), static_cast<unsigned>(s.n_layers));

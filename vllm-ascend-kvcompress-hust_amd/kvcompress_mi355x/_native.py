@@ -52,6 +52,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _p, _sz,
         ],
     ),
+    "kvc_offset_phases": (_i32, [_p, _i32, _i32, _i32, _p, _p, _i32, _p, _p, _p]),
+    "kvc_score_max_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "kvc_score_paged_max": (
+        _i32,
+        [
+            _p, _i32, _i32, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+            _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i64, _p, _i64, _i64, _i64, _p, _sz,
+        ],
+    ),
     "kvc_head_stats": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p]),
     "kvc_aggregate": (
         _i32,

@@ -82,27 +82,21 @@ def mean_phase_table(
     return cos, sin
 
 
-def score_paged_keys_mean_precomputed(
+def _single_layer_scoring(
     k_cache: torch.Tensor,
     source_block_ids: torch.Tensor,
     q_real: torch.Tensor,
     q_imag: torch.Tensor,
     frequency_scale: torch.Tensor,
     extra_coefficient: torch.Tensor,
-    phase_cos: torch.Tensor,
-    phase_sin: torch.Tensor,
     num_tokens: int,
     output: torch.Tensor,
     block_size: int,
-    rope_style: str,
-    *,
-    q_pass_mean: torch.Tensor | None = None,
-    rotary_dim: int | None = None,
-) -> bool:
-    """Score one layer's paged keys with precomputed phases (tri/kernels.py:247-317).
-
-    ``output`` is [kv_heads, queries_per_kv, >= num_tokens] float32 with
-    contiguous query rows, as in the reference workspace layout."""
+    q_pass_mean: torch.Tensor | None,
+    rotary_dim: int | None,
+) -> dict:
+    """Checks shared by the one-layer scorers; returns the launch arguments
+    that do not depend on the offset aggregation."""
     if block_size != 128:
         raise ValueError("the HIP scorer addresses 128-token cache blocks")
     dev.validate_cache(k_cache, "k_cache", block_size)
@@ -132,10 +126,6 @@ def score_paged_keys_mean_precomputed(
         dev.require_hip(t, name)
         if tuple(t.shape) != (kv_heads, qpk, freq):
             raise ValueError(f"{name} must have shape {(kv_heads, qpk, freq)}")
-    for name, t in (("phase_cos", phase_cos), ("phase_sin", phase_sin)):
-        dev.require_hip(t, name)
-        if t.numel() != freq:
-            raise ValueError(f"{name} must hold {freq} values")
     dev.require_hip(output, "output")
     dev.require_dtype(output, "output", torch.float32)
     if output.ndim != 3 or tuple(output.shape[:2]) != (kv_heads, qpk) or output.shape[2] < num_tokens:
@@ -152,50 +142,150 @@ def score_paged_keys_mean_precomputed(
     def f32(t: torch.Tensor) -> torch.Tensor:
         return t.to(dtype=torch.float32).contiguous()
 
-    layer_ptrs = dev.pointer_table([k_cache], device)
-    seq_lens = torch.tensor([num_tokens], dtype=torch.int32, device=device)
-    token_offsets = torch.tensor([0, num_tokens], dtype=torch.int64, device=device)
-    block_offsets = torch.tensor([0, blocks.numel()], dtype=torch.int64, device=device)
-    q_pass = f32(q_pass_mean) if q_pass_mean is not None else None
-    qr, qi, sc, ex = f32(q_real), f32(q_imag), f32(frequency_scale), f32(extra_coefficient)
-    pc, ps = f32(phase_cos.reshape(-1)), f32(phase_sin.reshape(-1))
-    ws_bytes = _native.load().kvc_score_workspace_bytes(1, kv_heads, head_dim, rotary, qpk, 1, max(num_tokens, 1))
+    return dict(
+        device=device,
+        kv_heads=kv_heads,
+        qpk=qpk,
+        freq=freq,
+        rotary=rotary,
+        head_dim=head_dim,
+        num_tokens=num_tokens,
+        blocks=blocks,
+        layer_ptrs=dev.pointer_table([k_cache], device),
+        seq_lens=torch.tensor([num_tokens], dtype=torch.int32, device=device),
+        token_offsets=torch.tensor([0, num_tokens], dtype=torch.int64, device=device),
+        block_offsets=torch.tensor([0, blocks.numel()], dtype=torch.int64, device=device),
+        calib=(f32(q_real), f32(q_imag), f32(frequency_scale), f32(extra_coefficient)),
+        q_pass=f32(q_pass_mean) if q_pass_mean is not None else None,
+    )
+
+
+def _launch_single_layer(entry: str, a: dict, k_cache, rope_style, phase_args: tuple, output, ws_bytes: int) -> None:
     if ws_bytes == 0:
         raise ValueError("unsupported scoring shape for the MI355X kernel")
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=a["device"])
+    qr, qi, sc, ex = a["calib"]
     _native.call(
-        "kvc_score_paged",
-        dev.stream_handle(device),
+        entry,
+        dev.stream_handle(a["device"]),
         dev.cache_dtype_code(k_cache.dtype),
         1,
-        dev.ptr(layer_ptrs),
+        dev.ptr(a["layer_ptrs"]),
         int(k_cache.shape[0]),
         int(k_cache.stride(0)),
-        kv_heads,
-        head_dim,
-        rotary,
-        qpk,
+        a["kv_heads"],
+        a["head_dim"],
+        a["rotary"],
+        a["qpk"],
         dev.rope_style_code(rope_style),
         1,
-        num_tokens,
-        dev.ptr(seq_lens),
-        dev.ptr(token_offsets),
-        dev.ptr(block_offsets),
-        dev.ptr(blocks),
+        a["num_tokens"],
+        dev.ptr(a["seq_lens"]),
+        dev.ptr(a["token_offsets"]),
+        dev.ptr(a["block_offsets"]),
+        dev.ptr(a["blocks"]),
         dev.ptr(qr),
         dev.ptr(qi),
         dev.ptr(sc),
         dev.ptr(ex),
-        dev.ptr(q_pass),
-        dev.ptr(pc),
-        dev.ptr(ps),
-        0,
+        dev.ptr(a["q_pass"]),
+        *phase_args,
         dev.ptr(output),
         0,
         1,
         int(output.stride(1)),
         dev.ptr(workspace),
         ws_bytes,
+    )
+
+
+def score_paged_keys_mean_precomputed(
+    k_cache: torch.Tensor,
+    source_block_ids: torch.Tensor,
+    q_real: torch.Tensor,
+    q_imag: torch.Tensor,
+    frequency_scale: torch.Tensor,
+    extra_coefficient: torch.Tensor,
+    phase_cos: torch.Tensor,
+    phase_sin: torch.Tensor,
+    num_tokens: int,
+    output: torch.Tensor,
+    block_size: int,
+    rope_style: str,
+    *,
+    q_pass_mean: torch.Tensor | None = None,
+    rotary_dim: int | None = None,
+) -> bool:
+    """Score one layer's paged keys with precomputed phases (tri/kernels.py:247-317).
+
+    ``output`` is [kv_heads, queries_per_kv, >= num_tokens] float32 with
+    contiguous query rows, as in the reference workspace layout."""
+    a = _single_layer_scoring(
+        k_cache, source_block_ids, q_real, q_imag, frequency_scale, extra_coefficient, num_tokens, output, block_size,
+        q_pass_mean, rotary_dim,
+    )
+    for name, t in (("phase_cos", phase_cos), ("phase_sin", phase_sin)):
+        dev.require_hip(t, name)
+        if t.numel() != a["freq"]:
+            raise ValueError(f"{name} must hold {a['freq']} values")
+    pc = phase_cos.reshape(-1).to(dtype=torch.float32).contiguous()
+    ps = phase_sin.reshape(-1).to(dtype=torch.float32).contiguous()
+    ws_bytes = _native.load().kvc_score_workspace_bytes(
+        1, a["kv_heads"], a["head_dim"], a["rotary"], a["qpk"], 1, max(a["num_tokens"], 1)
+    )
+    _launch_single_layer("kvc_score_paged", a, k_cache, rope_style, (dev.ptr(pc), dev.ptr(ps), 0), output, ws_bytes)
+    return True
+
+
+def score_paged_keys_max(
+    k_cache: torch.Tensor,
+    source_block_ids: torch.Tensor,
+    q_real: torch.Tensor,
+    q_imag: torch.Tensor,
+    frequency_scale: torch.Tensor,
+    extra_coefficient: torch.Tensor,
+    omega: torch.Tensor,
+    offsets: torch.Tensor,
+    round_start: int,
+    num_tokens: int,
+    output: torch.Tensor,
+    block_size: int,
+    rope_style: str,
+    *,
+    q_pass_mean: torch.Tensor | None = None,
+    rotary_dim: int | None = None,
+) -> bool:
+    """One layer's scores with the rotary term maximised over the offsets,
+    score_post_rope_keys(aggregation="max") (tri/scoring.py:84-97), which the
+    reference runs on the torch path only (tri/method.py:348-431).  Arguments
+    as score_paged_keys_mean_precomputed plus omega [F], offsets [O] and the
+    round start the phases are formed at."""
+    a = _single_layer_scoring(
+        k_cache, source_block_ids, q_real, q_imag, frequency_scale, extra_coefficient, num_tokens, output, block_size,
+        q_pass_mean, rotary_dim,
+    )
+    for name, t in (("omega", omega), ("offsets", offsets)):
+        dev.require_hip(t, name)
+    if omega.numel() != a["freq"]:
+        raise ValueError(f"omega must hold {a['freq']} values")
+    n_off = int(offsets.numel())
+    if n_off == 0:
+        raise ValueError("at least one offset is required")
+    device = a["device"]
+    om = omega.reshape(-1).to(dtype=torch.float32).contiguous()
+    off = offsets.reshape(-1).to(dtype=torch.float32).contiguous()
+    rs = torch.tensor([int(round_start)], dtype=torch.int64, device=device)
+    pc = torch.empty((n_off, a["freq"]), dtype=torch.float32, device=device)
+    ps = torch.empty_like(pc)
+    _native.call(
+        "kvc_offset_phases", dev.stream_handle(device), 1, 1, a["freq"], dev.ptr(rs), dev.ptr(off), n_off, dev.ptr(om),
+        dev.ptr(pc), dev.ptr(ps),
+    )
+    ws_bytes = _native.load().kvc_score_max_workspace_bytes(
+        1, a["kv_heads"], a["head_dim"], a["rotary"], a["qpk"], 1, max(a["num_tokens"], 1), n_off
+    )
+    _launch_single_layer(
+        "kvc_score_paged_max", a, k_cache, rope_style, (dev.ptr(pc), dev.ptr(ps), n_off, 0), output, ws_bytes
     )
     return True
 

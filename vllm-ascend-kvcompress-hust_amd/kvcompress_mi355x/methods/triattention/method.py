@@ -63,10 +63,6 @@ class TriAttentionMethod(KVCompressionMethod):
 
     def __init__(self, options: Mapping[str, JsonScalar], vllm_config: Any, model_shape: ModelShape) -> None:
         self.config = TriAttentionConfig.from_method_config(options)
-        if self.config.score_aggregation != "mean":
-            raise ValueError(
-                "score_aggregation 'max' is not implemented by the MI355X scorer; use 'mean'"
-            )
         self.vllm_config = vllm_config
         self.model_shape = model_shape
         self.calibration = CalibrationStats.load(self.config.stats_path)
@@ -162,6 +158,7 @@ class TriAttentionMethod(KVCompressionMethod):
             layer_aggregation=self.config.layer_aggregation,
             max_seqs=1,
             max_seq_len=max_len,
+            score_aggregation=self.config.score_aggregation,
         )
 
     # ------------------------------------------------------------ compress --

@@ -5,7 +5,9 @@ batch at once, the work the reference does per request in
 TriAttentionMethod._select_keep_indices and compress (tri/method.py:256-475):
 
   1. phase table      kvc_mean_phases      [n_seq, S, F]
+                      (kvc_offset_phases [n_seq, S, O, F] for score_aggregation "max")
   2. score            kvc_score_paged      raw scores (layout below) + partial sums
+                      (kvc_score_paged_max: maximum over the offsets)
   3. head statistics  kvc_head_stats       mean/var [S, n_seq, H_q]
   4. aggregate        kvc_aggregate        agg [sum N] (head max, layer mean, sanitise)
   5. select           kvc_select_keep      keep [n_seq, budget] ascending
@@ -176,6 +178,7 @@ class CompressionPipeline:
         max_seqs: int,
         max_seq_len: int,
         max_tokens: int | None = None,
+        score_aggregation: str = "mean",
     ) -> None:
         if not scoring_k_caches or len(scoring_k_caches) != tables.n_layers:
             raise ValueError("one scoring K cache per scoring layer is required")
@@ -190,6 +193,8 @@ class CompressionPipeline:
                 raise ValueError("cache base addresses and page strides must be 16-byte aligned")
         if layer_aggregation not in ("mean", "max"):
             raise ValueError(f"unsupported layer aggregation {layer_aggregation!r}")
+        if score_aggregation not in ("mean", "max"):
+            raise ValueError(f"unsupported score aggregation: {score_aggregation}")
         if policy not in POLICY_CODES:
             raise ValueError(f"unsupported position policy: {policy}")
         self.device = reference.device
@@ -214,6 +219,7 @@ class CompressionPipeline:
         self.policy = policy
         self.select_shape = "auto"  # "auto", "single" or "split" (kvc_select_keep / _split)
         self.layer_aggregation = layer_aggregation
+        self.score_aggregation = score_aggregation
         self.n_heads = tables.kv_heads * tables.qpk
         self.scoring_ptrs = dev.pointer_table(scoring_k_caches, self.device)
         self.k_ptrs = dev.pointer_table(k_caches, self.device)
@@ -226,7 +232,12 @@ class CompressionPipeline:
         s = self.tables.n_layers
         self.max_seqs, self.max_seq_len, self.max_tokens = int(max_seqs), int(max_seq_len), int(max_tokens)
         dev_ = self.device
-        self.phase_cos = torch.empty((self.max_seqs, s, self.tables.freq), dtype=torch.float32, device=dev_)
+        n_off = int(self.tables.offsets.numel())
+        if self.score_aggregation == "max":
+            # Per-offset phases [n_seq, S, O, F] (kvc_offset_phases).
+            self.phase_cos = torch.empty((self.max_seqs, s, n_off, self.tables.freq), dtype=torch.float32, device=dev_)
+        else:
+            self.phase_cos = torch.empty((self.max_seqs, s, self.tables.freq), dtype=torch.float32, device=dev_)
         self.phase_sin = torch.empty_like(self.phase_cos)
         layout = _native.load().kvc_score_raw_layout(
             dev.cache_dtype_code(self.dtype),
@@ -239,6 +250,11 @@ class CompressionPipeline:
         if layout < 0:
             _native.check(layout, "kvc_score_raw_layout")
         self.head_major = layout == _native.RAW_HEAD_MAJOR
+        if self.score_aggregation == "max" and not self.head_major:
+            raise ValueError(
+                "score_aggregation 'max' runs on the matrix-core scorer: bf16 or fp16 caches, head_dim 64, 128 or 256 "
+                "and rotary_dim/2 a multiple of 32"
+            )
         if self.head_major:
             # Token axis padded to 64 so every head row starts 256-byte aligned.
             padded = -(-self.max_tokens // 64) * 64
@@ -251,9 +267,11 @@ class CompressionPipeline:
         self.keep = torch.empty((self.max_seqs, self.budget), dtype=torch.int64, device=dev_)
         self.select_ws = select_workspace(self.max_seqs, self.segments, self.policy, dev_)
         self.layer_scores = None  # [S, max_tokens] per-layer head maxima, made on first use
-        ws = _native.load().kvc_score_workspace_bytes(
-            s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len
-        )
+        shape = (s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len)
+        if self.score_aggregation == "max":
+            ws = _native.load().kvc_score_max_workspace_bytes(*shape, n_off)
+        else:
+            ws = _native.load().kvc_score_workspace_bytes(*shape)
         if ws == 0:
             raise ValueError("unsupported scoring shape for the MI355X kernel")
         self.workspace_bytes = int(ws)
@@ -306,21 +324,28 @@ class CompressionPipeline:
         t = self.tables
         stream = dev.stream_handle(self.device)
         max_len = max(batch.seq_lens_host)
+        n_off = int(t.offsets.numel())
+        max_mode = self.score_aggregation == "max"
         _native.call(
-            "kvc_mean_phases",
+            "kvc_offset_phases" if max_mode else "kvc_mean_phases",
             stream,
             batch.n_seq,
             t.n_layers,
             t.freq,
             dev.ptr(batch.round_starts),
             dev.ptr(t.offsets),
-            int(t.offsets.numel()),
+            n_off,
             dev.ptr(t.omega),
             dev.ptr(self.phase_cos),
             dev.ptr(self.phase_sin),
         )
+        phase_args = (
+            (dev.ptr(self.phase_cos), dev.ptr(self.phase_sin), n_off, t.n_layers * n_off * t.freq)
+            if max_mode
+            else (dev.ptr(self.phase_cos), dev.ptr(self.phase_sin), t.n_layers * t.freq)
+        )
         _native.call(
-            "kvc_score_paged",
+            "kvc_score_paged_max" if max_mode else "kvc_score_paged",
             stream,
             dev.cache_dtype_code(self.dtype),
             t.n_layers,
@@ -343,9 +368,7 @@ class CompressionPipeline:
             dev.ptr(t.freq_scale),
             dev.ptr(t.extra),
             dev.ptr(t.q_pass),
-            dev.ptr(self.phase_cos),
-            dev.ptr(self.phase_sin),
-            t.n_layers * t.freq,
+            *phase_args,
             dev.ptr(self.raw),
             *self.raw_strides(),
             dev.ptr(self.workspace),

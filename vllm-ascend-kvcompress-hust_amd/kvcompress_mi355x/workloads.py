@@ -366,7 +366,7 @@ def move_cache(cache: SyntheticCache, device: torch.device | str) -> SyntheticCa
     )
 
 
-def build_pipeline(cache: SyntheticCache):
+def build_pipeline(cache: SyntheticCache, *, score_aggregation: str = "mean", layer_aggregation: str = "mean"):
     """CompressionPipeline + Batch over a synthetic cache (all sequences)."""
     from .methods.triattention.pipeline import Batch, CompressionPipeline, ScoringTables
     from .methods.triattention.scoring import build_geometric_offsets
@@ -387,10 +387,11 @@ def build_pipeline(cache: SyntheticCache):
         protected_recent=spec.recent,
         segments=spec.segments,
         policy=spec.policy,
-        layer_aggregation="mean",
+        layer_aggregation=layer_aggregation,
         max_seqs=len(spec.seq_lens),
         max_seq_len=max(spec.seq_lens),
         max_tokens=spec.total_tokens,
+        score_aggregation=score_aggregation,
     )
     batch = Batch.build(
         device,
