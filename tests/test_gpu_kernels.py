@@ -216,6 +216,33 @@ def test_score_paged_max_matches_oracle(hip_device, case) -> None:
     assert float((want - mean).abs().max()) > 1e-2
 
 
+def test_score_paged_max_nan_key(hip_device) -> None:
+    # A NaN key gives NaN for every offset, so its max-aggregated score is NaN
+    # (torch.maximum propagates it); other tokens and KV heads are unaffected.
+    kernels, _, _ = _kvc()
+    kv, qpk, head_dim, tokens = 2, 4, 128, 300
+    g = torch.Generator().manual_seed(99)
+    stats = _random_stats(g, kv, qpk, head_dim // 2, 0, head_dim)
+    cache = torch.randn(4, 128, kv, head_dim, generator=g).to(torch.bfloat16)
+    cache[1, 5, 0, 17] = float("nan")  # token 128 + 5 of KV head 0
+    blocks = torch.tensor([0, 1, 2])
+    offsets = ref.build_geometric_offsets(32768)
+    keys = ref.gather_paged_range(cache, blocks, start=0, count=tokens, block_size=128)
+    want = ref.score_post_rope_keys(keys, stats, round_start=tokens, offsets=offsets, aggregation="max")
+    out = torch.empty((kv, qpk, tokens), device=hip_device)
+    d = lambda t: t.to(hip_device)  # noqa: E731
+    assert kernels.score_paged_keys_max(
+        d(cache), d(blocks), d(stats.q_mean_real), d(stats.q_mean_imag), d(torch.sqrt(stats.freq_scale_sq)),
+        d(stats.q_abs_mean - torch.sqrt(stats.q_mean_real.square() + stats.q_mean_imag.square() + 1e-8)),
+        d(stats.omega), d(offsets), tokens, tokens, out, 128, "half",
+    )
+    got = out.cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(want))
+    assert int(torch.isnan(got).sum()) == qpk
+    keep = ~torch.isnan(want)
+    assert_scores_close(torch.where(keep, got, 0.0).reshape(kv * qpk, tokens), torch.where(keep, want, 0.0).reshape(kv * qpk, tokens))
+
+
 def test_offset_phase_table_matches_torch(hip_device) -> None:
     from kvcompress_mi355x import _native
     from kvcompress_mi355x.methods.triattention import _device as dev

@@ -5,14 +5,18 @@
 //         + sum_f a*extra*|k_f| + q_pass.k_pass,      phi_of = (o + rs) * omega_f.
 // For one offset the rotary term is a dot product of the key with per-offset
 // folded weights, kr*a(qr c - qi s) + ki*a(qi c + qr s), so every (query
-// head, offset) pair is one more column of the scoring GEMM.  Per query head
-// the offsets fill chunks of 16 B columns (columns past the last offset repeat
-// it, which leaves the maximum unchanged); a 16-token key tile times a chunk
-// gives D[token][offset] with the 16 offsets of a row in the 16 lanes of a DPP
-// row, so the maximum over offsets is an elementwise max across chunks and
-// four DPP steps inside the row.  The magnitude and pass terms do not depend
-// on the offset: they come from the mean scorer's fragments with the rotary
-// weights set to zero and are added after the maximum, as in the reference.
+// head, offset) pair is one row of a small GEMM against the keys.  Per query
+// head the offsets fill chunks of 16 rows (rows past the last offset repeat
+// it, which leaves the maximum unchanged).  The weights are the A operand and
+// the keys the B operand of v_mfma_f32_16x16x32_{bf16,f16}; a B operand lane
+// holds the same eight key values as an A operand lane of the mean scorer
+// (token l%16, dims 8*(l/16)..+8 of the K step), so the key loads are shared.
+// D[4*kb + i][t] is then offset 4*kb + i of token t: the maximum over a chunk
+// is three in-lane maxima and two exchanges across the four row blocks.  The
+// magnitude and pass terms do not depend on the offset: they come from the
+// mean scorer's fragments (rotary weights zero) in the same transposed form,
+// D[4*kb + i][t] = query head 4*kb + i, and are added after the maximum, as
+// in the reference.
 //
 // Work split: a workgroup owns one KV head, a group of its query heads (all of
 // them when their fragments fit the LDS budget) and KVC_MAX_SPANS consecutive
@@ -21,10 +25,12 @@
 // chunk) are staged in LDS once per workgroup; each fragment read feeds two
 // key tiles.  Workgroups that share a key span but not a query-head group are
 // placed eight apart in the grid, on the same XCD, so the second read of the
-// keys is an L2 hit.  Raw scores, partial sums and the stage epilogue are the
-// mean scorer's.
+// keys is an L2 hit.  Raw scores and partial sums have the mean scorer's
+// layout, so kvc_head_stats and kvc_aggregate are shared.
 
 #include <math.h>
+
+#include <type_traits>
 
 #include "mfma_common.h"
 
@@ -63,10 +69,10 @@ __device__ __forceinline__ float offset_weight(const FoldArgs& a, int b, int lay
 }
 
 // One wave per column (sequence, layer, KV head, query head g).  Lane l owns
-// B-operand lane l of every (chunk, step) fragment: offset column 16*chunk +
+// A-operand lane l of every (chunk, step) fragment: offset row 16*chunk +
 // l%16 (clamped to the last offset), rotary dims 32*step + 8*(l/16) + e.  fp16
-// columns are scaled by the power of two that brings their largest weight to
-// [2^13, 2^14), as the mean scorer's fp16 fold does.
+// weights of a query head are scaled by the power of two that brings the
+// largest to [2^13, 2^14), as the mean scorer's fp16 fold does.
 template <bool F16>
 __global__ __launch_bounds__(256) void fold_offsets_kernel(OffsetFoldArgs m) {
   typedef MfmaElem<F16> E;
@@ -125,6 +131,14 @@ __global__ __launch_bounds__(256) void fold_offsets_kernel(OffsetFoldArgs m) {
   if (lane == 0) m.inv_scale[col] = F16 ? ldexpf(1.0f, -sh) : 1.0f;
 }
 
+// Keys of pages the block table does not resolve read as zeros from here
+// (the furthest load reads 16 bytes at element 32 * (NK - 1) + 24).
+__device__ __attribute__((aligned(16))) uint32_t kZeroKeys[8 * 16];
+
+// IEEE 754-2019 maximum: NaN if either input is NaN, as torch.maximum
+// (one v_maximum3_f32 on gfx950).
+__device__ __forceinline__ float max_prop(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 struct MaxGeometry {
   int gpg;     // query heads per workgroup
   int groups;  // query-head groups per KV head
@@ -132,16 +146,7 @@ struct MaxGeometry {
   int work;    // (span set, KV head) items
 };
 
-// Maximum over the 16 lanes of a DPP row (NaN-propagating, as torch.maximum).
-__device__ __forceinline__ float row16_max(float v) {
-  v = max_nan(v, dpp_quad_xor1(v));
-  v = max_nan(v, dpp_quad_xor2(v));
-  v = max_nan(v, dpp_row_half_mirror(v));
-  v = max_nan(v, dpp_row_mirror(v));
-  return v;
-}
-
-template <int NK, int NF, bool F16, bool IL>
+template <int NK, int NF, int NCH, bool F16, bool IL>
 __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, MaxGeometry geo, int qpk,
                                                                   const u32x4* __restrict__ rest_frags,
                                                                   const float* __restrict__ rest_scale,
@@ -149,10 +154,11 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
                                                                   const float* __restrict__ off_scale) {
   typedef MfmaElem<F16> E;
   typedef typename E::vec vec_t;
-  constexpr int NR = 2 * NF;                    // rotary K steps of 32 dims
-  constexpr int NP = NK - NR;                   // pass K steps
+  constexpr int NR = 2 * NF;   // rotary K steps of 32 dims
+  constexpr int NP = NK - NR;  // pass K steps
   constexpr int kNP = NP > 0 ? NP : 1;
-  extern __shared__ u32x4 lds_frag[];           // [gpg][nch][NR][hi/lo][64]
+  constexpr int kStreams = kScoreThreads / 64;
+  extern __shared__ u32x4 lds_frag[];  // [gpg][NCH][NR][hi/lo][64]
 
   // blockIdx.x = ((item / 8) * groups + group) * 8 + item % 8: the groups of
   // one item are eight workgroups apart (same XCD).
@@ -172,28 +178,29 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int r = lane & 15;   // A row (token in tile) / D column
-  const int kb = lane >> 4;  // K block of A/B, row block of D
+  const int r = lane & 15;   // token of the tile (B column / D column)
+  const int kb = lane >> 4;  // K block of the operands, row block of D
   const int64_t col0 = ((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * qpk;
-  const int frag_per_g = geo.nch * NR * 2 * 64;
+  constexpr int kFragPerG = NCH * NR * 2 * 64;
 
   // Stage this group's per-offset fragments.
   {
-    const u32x4* src = off_frags + (col0 + g0) * frag_per_g;
-    const int count = gcnt * frag_per_g;
+    const u32x4* src = off_frags + (col0 + g0) * kFragPerG;
+    const int count = gcnt * kFragPerG;
 #pragma unroll 4
     for (int i = threadIdx.x; i < count; i += kScoreThreads) lds_frag[i] = src[i];
   }
 
-  // Magnitude and pass fragments (packed [frag][kb][g < qpk], rotary weights zero).
+  // Magnitude and pass fragments (packed [frag][kb][g < qpk], rotary weights
+  // zero), used as A operands: lane (kb, r) holds row r = query head.
   constexpr int kFrags = 2 * NK + 2 * NF;
   const int packed = 4 * qpk;
-  const bool live_col = r < qpk;
+  const bool live_row = r < qpk;
   const u32x4* fp = rest_frags + (((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * kFrags) * packed +
-                    kb * qpk + (live_col ? r : 0);
+                    kb * qpk + (live_row ? r : 0);
   auto frag_word = [&](int f) {
     const u32x4 v = fp[f * packed];
-    return __builtin_bit_cast(vec_t, live_col ? v : u32x4{0, 0, 0, 0});
+    return __builtin_bit_cast(vec_t, live_row ? v : u32x4{0, 0, 0, 0});
   };
   vec_t p_hi[kNP], p_lo[kNP], m_hi[NF], m_lo[NF];
 #pragma unroll
@@ -206,8 +213,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     m_hi[q] = frag_word(2 * NK + 2 * q);
     m_lo[q] = frag_word(2 * NK + 2 * q + 1);
   }
-  const float r_scale = F16 ? rest_scale[col0 + (live_col ? r : 0)] : 1.0f;
-  const float o_scale = F16 ? off_scale[col0 + (live_col ? r : 0)] : 1.0f;
+  // Output heads of this lane: D rows 4*kb + i.  fp16 column scales per head.
+  float r_scale[4], o_scale[4];
+  bool writes[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * kb + i;
+    writes[i] = h >= g0 && h < g0 + gcnt;
+    r_scale[i] = F16 && h < qpk ? rest_scale[col0 + h] : 1.0f;
+    o_scale[i] = F16 && h < qpk ? off_scale[col0 + h] : 1.0f;
+  }
 
   KVC_GLOBAL const uint16_t* kbase = gptr_from_int<const uint16_t>(a.k_layer_ptrs[layer]);
   const int64_t* bt = a.block_ids + a.block_offsets[b];
@@ -216,14 +231,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
   const int64_t lane_off = static_cast<int64_t>(head) * a.head_dim + 8 * kb;
   const int64_t tok_base = a.token_offsets[b];
   float* raw_out = a.raw + layer * a.raw_layer_stride;
-  const bool writer = r >= g0 && r < g0 + gcnt;
 
-  __shared__ __attribute__((aligned(16))) float stage[kMfmaMaxQpk * kStageStride];
-  __shared__ double red[2][kScoreThreads];
-  float* stage_row = stage + (writer ? r - g0 : 0) * kStageStride;
+  // Score stage: one row per query head of the group and a spare row that
+  // takes the stores of lanes without a head in the group.
+  __shared__ __attribute__((aligned(16))) float stage[(kMfmaMaxQpk + 1) * kStageStride];
+  float* stage_rows[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) stage_rows[i] = stage + (writes[i] ? 4 * kb + i - g0 : kMfmaMaxQpk) * kStageStride + r;
   __syncthreads();  // fragments staged
 
-  // Magnitude + pass term of a tile: D[4*kb + i][r] for query head r.
+  // Magnitude + pass term of a tile: D[4*kb + i][r] = query head 4*kb + i, token r.
   auto rest_tile = [&](const u32x4 (&ka)[NK]) {
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -231,135 +248,177 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     for (int j = 0; j < NP; ++j) {
       const vec_t kv = __builtin_bit_cast(vec_t, ka[NR + j]);
       if (j & 1) {
-        acc1 = E::mfma(kv, p_hi[j], acc1);
-        acc1 = E::mfma(kv, p_lo[j], acc1);
+        acc1 = E::mfma(p_hi[j], kv, acc1);
+        acc1 = E::mfma(p_lo[j], kv, acc1);
       } else {
-        acc0 = E::mfma(kv, p_hi[j], acc0);
-        acc0 = E::mfma(kv, p_lo[j], acc0);
+        acc0 = E::mfma(p_hi[j], kv, acc0);
+        acc0 = E::mfma(p_lo[j], kv, acc0);
       }
     }
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
       vec_t khi, klo;
       magnitude_operands<F16, IL, NK, NF>(ka, q, &khi, &klo);
-      acc0 = E::mfma(khi, m_hi[q], acc0);
-      acc1 = E::mfma(khi, m_lo[q], acc1);
-      acc0 = E::mfma(klo, m_hi[q], acc0);
+      acc0 = E::mfma(m_hi[q], khi, acc0);
+      acc1 = E::mfma(m_lo[q], khi, acc1);
+      acc0 = E::mfma(m_hi[q], klo, acc0);
     }
     return acc0 + acc1;
   };
 
-  for (int sp = 0; sp < kMaxSpans; ++sp) {
+  // D[4*kb + i][r] of one offset chunk holds offset 16c + 4*kb + i of token r:
+  // the maximum over a chunk is three in-lane maxima and two exchanges across
+  // the row blocks.  v_permlane32_swap / v_permlane16_swap of a value with
+  // itself leave lanes l and l^32 (l^16) holding the pair {x_l, x_(l^32)} in
+  // some order, so a maximum of the two results is the exchange-and-max.
+  auto token_max = [&](const f32x4& v) {
+    float m = max_prop(max_prop(v[0], v[1]), max_prop(v[2], v[3]));
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = max_prop(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return max_prop(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+  };
+
+  // Keys of a 16-token tile of the span starting at token st0.  Tiles past the
+  // span re-read its last tile and rows past the sequence read whatever their
+  // page holds: a token is a column of every product here, so those rows only
+  // reach scores that are never stored.  Unresolved pages read as zeros.
+  auto load_tile = [&](const SpanPages& pg, int st0, int st1, int mt, u32x4 (&ka)[NK]) {
+    const int smt = (st1 - st0 + 15) / 16;
+    const int mt_read = mt < smt ? mt : smt - 1;
+    const int rel = mt_read * 16 + r;
+    const int t = st0 + rel;
+    bool page_ok = false;
+    KVC_GLOBAL const uint16_t* pbase = pg.page(rel, &page_ok);
+    KVC_GLOBAL const uint16_t* row =
+        page_ok ? pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off
+                : reinterpret_cast<KVC_GLOBAL const uint16_t*>(gptr(kZeroKeys));
+#pragma unroll
+    for (int j = 0; j < NK; ++j) ka[j] = load_k(reinterpret_cast<KVC_GLOBAL const u32x4*>(row + 32 * j));
+  };
+
+  // Wave w scores tiles (w, w+4) and (w+8, w+12) of every span; the keys of
+  // the next pair, also across a span boundary and the span's epilogue, are in
+  // flight while a pair is scored.
+  static_assert(kScoreTile == 16 * 4 * kStreams, "two pairs of tiles per wave cover a span");
+  const int n_sp = min(kMaxSpans, (n - tile_first * kScoreTile + kScoreTile - 1) / kScoreTile);
+  u32x4 ka[2][NK], kn[2][NK];
+  SpanPages pages;
+  pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, tile_first * kScoreTile);
+  {
+    const int st0 = tile_first * kScoreTile;
+    const int st1 = min(n, st0 + kScoreTile);
+    load_tile(pages, st0, st1, wave, ka[0]);
+    load_tile(pages, st0, st1, wave + kStreams, ka[1]);
+  }
+  for (int sp = 0; sp < n_sp; ++sp) {
     const int tile = tile_first + sp;
     const int t0 = tile * kScoreTile;
-    if (t0 >= n) break;  // the same for every wave
     const int t1 = min(n, t0 + kScoreTile);
     const int n_mt = (t1 - t0 + 15) / 16;
-    SpanPages pages;
-    pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0);
-
-    auto load_tile = [&](int mt, u32x4 (&ka)[NK]) {
-      // Unconditional loads of rows inside the pool, as in the mean scorer:
-      // tiles past the span re-read its last tile, unresolved pages read page
-      // 0, and both are zeroed.
-      const int mt_read = mt < n_mt ? mt : n_mt - 1;
-      const int rel = mt_read * 16 + r;
-      const int t = t0 + rel;
-      bool page_ok = false;
-      KVC_GLOBAL const uint16_t* pbase = pages.page(rel, &page_ok);
-      const bool ok = mt < n_mt && t < t1 && page_ok;
-      KVC_GLOBAL const uint16_t* row = pbase + static_cast<int64_t>(t & (kBlockSize - 1)) * row_elems + lane_off;
-#pragma unroll
-      for (int j = 0; j < NK; ++j) {
-        const u32x4 v = load_k(reinterpret_cast<KVC_GLOBAL const u32x4*>(row + 32 * j));
-        ka[j] = ok ? v : u32x4{0, 0, 0, 0};
-      }
-    };
-
-    double sum = 0.0, sumsq = 0.0;
+    const bool more = sp + 1 < n_sp;
+    SpanPages next;  // pages past the table resolve as missing; unused after the last span
+    next.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0 + kScoreTile);
+    // Column 16*mt + r of the lane's four head rows (columns past the span
+    // are never read back).
     auto emit = [&](int mt, const f32x4& v) {
-      const int rel = mt * 16 + 4 * kb;
-      if (writer && mt < n_mt) {
-        *reinterpret_cast<f32x4*>(stage_row + rel) = v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (t0 + rel + i < t1) {
-            const double dv = static_cast<double>(v[i]);
-            sum += dv;
-            sumsq = fma(dv, dv, sumsq);
-          }
-        }
-      }
+      for (int i = 0; i < 4; ++i) stage_rows[i][mt * 16] = v[i];
     };
 
-    // Two tiles per pass over the staged fragments.
+    // Two tiles per pass over the staged fragments.  The maximum of query
+    // head g is reduced while the MFMAs of head g + 1 run.
     auto score_pair = [&](int mt0, const u32x4 (&k0)[NK], int mt1, const u32x4 (&k1)[NK]) {
       const f32x4 rest0 = rest_tile(k0);
       const f32x4 rest1 = rest_tile(k1);
       f32x4 mx0 = {0.0f, 0.0f, 0.0f, 0.0f}, mx1 = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int gl = 0; gl < gcnt; ++gl) {
-        f32x4 best0 = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, best1 = best0;
-        for (int c = 0; c < geo.nch; ++c) {
-          const u32x4* wl = lds_frag + ((gl * geo.nch + c) * NR) * 128 + lane;
-          f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
-          f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int st = 0; st < NR; ++st) {
-            const vec_t whi = __builtin_bit_cast(vec_t, wl[st * 128]);
-            const vec_t wlo = __builtin_bit_cast(vec_t, wl[st * 128 + 64]);
-            const vec_t x0 = __builtin_bit_cast(vec_t, k0[st]);
-            const vec_t x1 = __builtin_bit_cast(vec_t, k1[st]);
-            acc0 = E::mfma(x0, whi, acc0);
-            acc1 = E::mfma(x1, whi, acc1);
-            acc0 = E::mfma(x0, wlo, acc0);
-            acc1 = E::mfma(x1, wlo, acc1);
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            best0[i] = max_nan(best0[i], acc0[i]);
-            best1[i] = max_nan(best1[i], acc1[i]);
-          }
-        }
-        const bool mine = r == g0 + gl;
+      f32x4 pend0 = {0.0f, 0.0f, 0.0f, 0.0f}, pend1 = pend0;
+      int pend_g = -1;  // no lane takes head -1
+      auto retire = [&]() {
+        const float v0 = token_max(pend0);
+        const float v1 = token_max(pend1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float v0 = row16_max(best0[i]);
-          const float v1 = row16_max(best1[i]);
+          const bool mine = 4 * kb + i == pend_g;
           mx0[i] = mine ? v0 : mx0[i];
           mx1[i] = mine ? v1 : mx1[i];
         }
+      };
+      // One item = one 16-offset chunk of one query head: 2*NR fragment
+      // reads and 4*NR MFMAs.  Items alternate between two register buffers
+      // so the next item's fragments are read while this item's MFMAs run.
+      f32x4 best0, best1;
+      auto item = [&](auto parity, int it, const vec_t (&w)[2 * NR]) {
+        constexpr int P = decltype(parity)::value;
+        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < NR; ++st) {
+          const vec_t x0 = __builtin_bit_cast(vec_t, k0[st]);
+          const vec_t x1 = __builtin_bit_cast(vec_t, k1[st]);
+          acc0 = E::mfma(w[2 * st], x0, acc0);
+          acc1 = E::mfma(w[2 * st], x1, acc1);
+          acc0 = E::mfma(w[2 * st + 1], x0, acc0);
+          acc1 = E::mfma(w[2 * st + 1], x1, acc1);
+        }
+        if constexpr (NCH == 1 || P == 0) {
+          best0 = acc0;
+          best1 = acc1;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            best0[i] = max_prop(best0[i], acc0[i]);
+            best1[i] = max_prop(best1[i], acc1[i]);
+          }
+        }
+        if constexpr (NCH == 1 || P == 1) {
+          retire();
+          pend0 = best0;
+          pend1 = best1;
+          pend_g = g0 + it / NCH;
+        }
+      };
+      const int n_items = gcnt * NCH;
+      auto load_w = [&](int it, vec_t (&w)[2 * NR]) {
+        const u32x4* wl = lds_frag + (min(it, n_items - 1) * NR) * 128 + lane;
+#pragma unroll
+        for (int st = 0; st < NR; ++st) {
+          w[2 * st] = __builtin_bit_cast(vec_t, wl[st * 128]);
+          w[2 * st + 1] = __builtin_bit_cast(vec_t, wl[st * 128 + 64]);
+        }
+      };
+      vec_t wa[2 * NR], wb[2 * NR];
+      load_w(0, wa);
+      int it = 0;
+      for (; it + 1 < n_items; it += 2) {
+        load_w(it + 1, wb);
+        item(std::integral_constant<int, 0>{}, it, wa);
+        load_w(it + 2, wa);
+        item(std::integral_constant<int, 1>{}, it + 1, wb);
       }
+      if (it < n_items) item(std::integral_constant<int, 0>{}, it, wa);  // odd count: NCH == 1 only
+      retire();
       f32x4 out0, out1;
-      if (F16) {
-        out0 = mx0 * o_scale + rest0 * r_scale;
-        out1 = mx1 * o_scale + rest1 * r_scale;
-      } else {
-        out0 = mx0 + rest0;
-        out1 = mx1 + rest1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out0[i] = F16 ? mx0[i] * o_scale[i] + rest0[i] * r_scale[i] : mx0[i] + rest0[i];
+        out1[i] = F16 ? mx1[i] * o_scale[i] + rest1[i] * r_scale[i] : mx1[i] + rest1[i];
       }
       emit(mt0, out0);
       emit(mt1, out1);
     };
 
-    // Wave w scores tiles w, w+4, w+8, ... in pairs (w, w+4), (w+8, w+12);
-    // the next pair's keys are in flight while the current pair is scored.
-    constexpr int kStreams = kScoreThreads / 64;
-    u32x4 ka[2][NK], kn[2][NK];
-    int mt = wave;
-    load_tile(mt, ka[0]);
-    load_tile(mt + kStreams, ka[1]);
-    for (; mt < n_mt; mt += 4 * kStreams) {
-      load_tile(mt + 2 * kStreams, kn[0]);
-      load_tile(mt + 3 * kStreams, kn[1]);
-      score_pair(mt, ka[0], mt + kStreams, ka[1]);
-      if (mt + 2 * kStreams >= n_mt) break;
-      load_tile(mt + 4 * kStreams, ka[0]);
-      load_tile(mt + 5 * kStreams, ka[1]);
-      score_pair(mt + 2 * kStreams, kn[0], mt + 3 * kStreams, kn[1]);
+    load_tile(pages, t0, t1, wave + 2 * kStreams, kn[0]);
+    load_tile(pages, t0, t1, wave + 3 * kStreams, kn[1]);
+    if (wave < n_mt) score_pair(wave, ka[0], wave + kStreams, ka[1]);
+    if (more) {
+      const int nt0 = t0 + kScoreTile;
+      const int nt1 = min(n, nt0 + kScoreTile);
+      load_tile(next, nt0, nt1, wave, ka[0]);
+      load_tile(next, nt0, nt1, wave + kStreams, ka[1]);
     }
+    if (wave + 2 * kStreams < n_mt) score_pair(wave + 2 * kStreams, kn[0], wave + 3 * kStreams, kn[1]);
 
-    red[0][threadIdx.x] = sum;
-    red[1][threadIdx.x] = sumsq;
     __syncthreads();
 
     // Stage -> raw scores (rows g0 .. g0+gcnt-1 of this KV head), as the mean scorer.
@@ -386,39 +445,57 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
             stage[row * kStageStride + t];
       }
     }
-    // Partial sums of query head g: lanes 16k + g of the four waves.
-    for (int i = threadIdx.x; i < gcnt; i += kScoreThreads) {
-      const int g = g0 + i;
+    // Per-head float64 sums of the span's scores for kvc_head_stats: wave w
+    // takes rows w, w+4, ...; lane l sums tokens l, l+64, l+128, l+192.
+    for (int row = wave; row < gcnt; row += kStreams) {
       double s0 = 0.0, s1 = 0.0;
-      for (int w = 0; w < kStreams; ++w) {
-        for (int k = 0; k < 4; ++k) {
-          s0 += red[0][w * 64 + k * 16 + g];
-          s1 += red[1][w * 64 + k * 16 + g];
+#pragma unroll
+      for (int k = 0; k < kScoreTile / 64; ++k) {
+        const int c = lane + 64 * k;
+        if (c < span) {
+          const double dv = static_cast<double>(stage[row * kStageStride + c]);
+          s0 += dv;
+          s1 = fma(dv, dv, s1);
         }
       }
-      const int n_heads = a.kv_heads * qpk;
-      double* dst = a.partials +
-                    (((static_cast<int64_t>(layer) * a.n_seq + b) * a.max_tiles + tile) * n_heads + head * qpk + g) * 2;
-      dst[0] = s0;
-      dst[1] = s1;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        s0 += __shfl_xor(s0, off);
+        s1 += __shfl_xor(s1, off);
+      }
+      if (lane == 0) {
+        const int n_heads = a.kv_heads * qpk;
+        double* dst = a.partials +
+                      (((static_cast<int64_t>(layer) * a.n_seq + b) * a.max_tiles + tile) * n_heads + q_first + row) * 2;
+        dst[0] = s0;
+        dst[1] = s1;
+      }
     }
     __syncthreads();  // stage and red are reused by the next span
+    pages = next;
   }
 }
 
 using MaxKernel = void (*)(ScoreArgs, MaxGeometry, int, const u32x4*, const float*, const u32x4*, const float*);
 
-template <bool F16, bool IL>
-MaxKernel pick_max_typed(int nk, int nf) {
+template <int NCH, bool F16, bool IL>
+MaxKernel pick_max_chunks(int nk, int nf) {
   switch (nk * 16 + nf) {
-    case 2 * 16 + 1: return score_max_kernel<2, 1, F16, IL>;
-    case 4 * 16 + 1: return score_max_kernel<4, 1, F16, IL>;
-    case 4 * 16 + 2: return score_max_kernel<4, 2, F16, IL>;
-    case 8 * 16 + 1: return score_max_kernel<8, 1, F16, IL>;
-    case 8 * 16 + 2: return score_max_kernel<8, 2, F16, IL>;
-    case 8 * 16 + 4: return score_max_kernel<8, 4, F16, IL>;
+    case 2 * 16 + 1: return score_max_kernel<2, 1, NCH, F16, IL>;
+    case 4 * 16 + 1: return score_max_kernel<4, 1, NCH, F16, IL>;
+    case 4 * 16 + 2: return score_max_kernel<4, 2, NCH, F16, IL>;
+    case 8 * 16 + 1: return score_max_kernel<8, 1, NCH, F16, IL>;
+    case 8 * 16 + 2: return score_max_kernel<8, 2, NCH, F16, IL>;
+    case 8 * 16 + 4: return score_max_kernel<8, 4, NCH, F16, IL>;
     default: return nullptr;
   }
+}
+
+template <bool F16, bool IL>
+MaxKernel pick_max_typed(int nk, int nf, int nch) {
+  if (nch == 1) return pick_max_chunks<1, F16, IL>(nk, nf);
+  if (nch == 2) return pick_max_chunks<2, F16, IL>(nk, nf);
+  return nullptr;
 }
 
 }  // namespace
@@ -427,11 +504,14 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
                       const ScoreArgs& sa, void* workspace) {
   const int nk = s.head_dim / 32, nf = s.freq / 32, nr = 2 * nf;
   const bool f16 = dtype == KVC_DTYPE_FP16;
-  MaxKernel kern = f16 ? (fa.interleaved ? pick_max_typed<true, true>(nk, nf) : pick_max_typed<true, false>(nk, nf))
-                       : (fa.interleaved ? pick_max_typed<false, true>(nk, nf) : pick_max_typed<false, false>(nk, nf));
-  if (!kern) return fail(KVC_EINVAL, "kvc_score_paged_max: no scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
   MaxGeometry geo;
   geo.nch = offset_chunks(n_offsets);
+  if (geo.nch > 2)
+    return fail(KVC_EINVAL, "kvc_score_paged_max: at most 32 offsets (got %d; 2^0 .. 2^30 are 31)", n_offsets);
+  const int nch = geo.nch;
+  MaxKernel kern = f16 ? (fa.interleaved ? pick_max_typed<true, true>(nk, nf, nch) : pick_max_typed<true, false>(nk, nf, nch))
+                       : (fa.interleaved ? pick_max_typed<false, true>(nk, nf, nch) : pick_max_typed<false, false>(nk, nf, nch));
+  if (!kern) return fail(KVC_EINVAL, "kvc_score_paged_max: no scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
   const int per_g = geo.nch * nr * 2 * kOffsetFragBytes;
   int gpg = kMaxFragLds / per_g;
   if (gpg < 1)
