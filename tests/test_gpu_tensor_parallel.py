@@ -113,3 +113,108 @@ def test_kv_head_shards_reproduce_the_unsharded_step(hip_device, config, overrid
                 assert torch.equal(ks[layer], cache.k_caches[layer][:, :, heads, :]), f"rank {r} K layer {layer}"
                 assert torch.equal(vs[layer], cache.v_caches[layer][:, :, heads, :]), f"rank {r} V layer {layer}"
     assert near <= 4
+
+
+def _free_port() -> int:
+    import socket
+
+    with socket.socket(socket.AF_INET, socket.SOCK_STREAM) as s:
+        s.bind(("127.0.0.1", 0))
+        return int(s.getsockname()[1])
+
+
+def test_method_with_tensor_parallel_ranks(hip_device, tmp_path) -> None:
+    """TriAttentionMethod at tensor_parallel_size 2: two rank processes on this
+    GPU, each bound to half of the KV heads, meet in one MAX all-reduce over a
+    gloo group (tri/method.py:106-122,315-322,447-461).  Both must select the
+    keep set of the unsharded method and compact their heads exactly as the
+    unsharded compaction does."""
+    import json
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    from types import SimpleNamespace
+
+    from kvcompress_mi355x import workloads
+    from kvcompress_mi355x.methods import create_method
+    from kvcompress_mi355x.methods.base import CompressionRequest, LayerCache
+    from kvcompress_mi355x.methods.triattention.cache import token_slots
+
+    overrides = dict(n_layers=4, score_layer_stride=2, seq_lens=(8192,), budget=2048, recent=128, max_model_len=16384)
+    spec = workloads.config_spec(2, **overrides)
+    host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
+    stats_path = tmp_path / "stats.pt"
+    torch.save(
+        {
+            "metadata": dict(host.calibration.metadata),
+            "layer_stats": {
+                i: {
+                    "q_mean_real": s.q_mean_real,
+                    "q_mean_imag": s.q_mean_imag,
+                    "q_abs_mean": s.q_abs_mean,
+                    "freq_scale_sq": s.freq_scale_sq,
+                }
+                for i, s in host.calibration.layers.items()
+            },
+        },
+        stats_path,
+    )
+    options = {"stats_path": str(stats_path), "kv_budget": 2048, "score_layer_stride": 2, "protected_recent_window": 128}
+    job = tmp_path / "job.json"
+    job.write_text(json.dumps({"config": 2, "overrides": overrides, "options": options}))
+
+    # The two ranks, as separate processes sharing this GPU.
+    world, port = 2, _free_port()
+    worker = Path(__file__).resolve().parent / "tp_rank_worker.py"
+    env = dict(os.environ, MASTER_ADDR="127.0.0.1")
+    procs, logs = [], []
+    for r in range(world):
+        log = open(tmp_path / f"rank{r}.log", "w")
+        logs.append(log)
+        procs.append(subprocess.Popen(
+            [sys.executable, "-u", str(worker), "--rank", str(r), "--world", str(world), "--port", str(port),
+             "--job", str(job), "--out", str(tmp_path / f"rank{r}.pt")],
+            stdout=log, stderr=subprocess.STDOUT, env=env,
+        ))
+
+    # Meanwhile the unsharded method on the full cache in this process.
+    cache = workloads.move_cache(host, hip_device)
+    vllm_config = SimpleNamespace(
+        parallel_config=SimpleNamespace(tensor_parallel_size=1),
+        model_config=SimpleNamespace(max_model_len=spec.max_model_len),
+        speculative_config=None,
+    )
+    method = create_method("triattention", options, vllm_config, spec.model_shape())
+    layers = tuple(LayerCache(f"model.layers.{i}.self_attn.attn", i, cache.k_caches[i], cache.v_caches[i]) for i in range(spec.n_layers))
+    method.bind_model_runner(SimpleNamespace(device=hip_device), layers)
+    src, dst = cache.source_tables[0], cache.destination_tables[0]
+    n, rs = spec.seq_lens[0], host.round_starts[0]
+    keep_full = method.select_keep_indices(src, n, rs).cpu()
+    method.compress(CompressionRequest(
+        request_id="r0", semantic_num_tokens=rs, physical_num_tokens=n,
+        source_block_ids=(tuple(src.cpu().tolist()),), destination_block_ids=(tuple(dst.cpu().tolist()),),
+        source_block_ids_device=src, destination_block_ids_device=dst,
+    ))
+    torch.cuda.synchronize()
+    slots = token_slots(dst, torch.arange(spec.budget, device=hip_device), 128)
+    k_full = torch.stack([k.view(-1, spec.num_kv_heads, spec.head_dim)[slots] for k in cache.k_caches]).cpu()
+    v_full = torch.stack([v.view(-1, spec.num_kv_heads, spec.head_dim)[slots] for v in cache.v_caches]).cpu()
+
+    for r, proc in enumerate(procs):
+        try:
+            rc = proc.wait(timeout=300)
+        except subprocess.TimeoutExpired:
+            for p in procs:
+                p.kill()
+            pytest.fail(f"rank {r} did not finish")
+        logs[r].close()
+        assert rc == 0, f"rank {r} failed:\n" + (tmp_path / f"rank{r}.log").read_text()[-3000:]
+    local = spec.num_kv_heads // world
+    for r in range(world):
+        got = torch.load(tmp_path / f"rank{r}.pt", weights_only=True)
+        assert got["budget"] == spec.budget
+        assert torch.equal(got["keep"], keep_full), f"rank {r}: keep set differs from the unsharded method"
+        heads = slice(r * local, (r + 1) * local)
+        assert torch.equal(got["k"], k_full[:, :, heads]), f"rank {r}: compacted K differs"
+        assert torch.equal(got["v"], v_full[:, :, heads]), f"rank {r}: compacted V differs"

@@ -32,7 +32,7 @@ from ..base import (
 )
 from . import _device as dev
 from .config import TriAttentionConfig
-from .pipeline import Batch, CompressionPipeline, ScoringTables
+from .pipeline import Batch, CompressionPipeline, ScoringTables, max_all_reducer
 from .scoring import build_geometric_offsets
 from .stats import CalibrationStats, DeviceLayerCalibrationStats
 
@@ -71,6 +71,8 @@ class TriAttentionMethod(KVCompressionMethod):
         self.cache_block_size = KERNEL_BLOCK_SIZE
         self.offsets: torch.Tensor | None = None
         self.pipeline: CompressionPipeline | None = None
+        self.tensor_parallel_size = 1
+        self.all_reduce_max = None  # the TP group's MAX all-reduce when tensor_parallel_size > 1
 
     @property
     def name(self) -> str:
@@ -93,13 +95,25 @@ class TriAttentionMethod(KVCompressionMethod):
     # ---------------------------------------------------------------- bind --
     def bind_model_runner(self, runner: Any, layer_caches: tuple[LayerCache, ...]) -> None:
         tp_size = int(getattr(getattr(self.vllm_config, "parallel_config", None), "tensor_parallel_size", 1))
-        if tp_size != 1:
-            raise RuntimeError("the MI355X TriAttention path runs on one GPU (tensor_parallel_size 1)")
+        if tp_size < 1:
+            raise RuntimeError(f"invalid tensor_parallel_size {tp_size}")
+        tp_rank = 0
+        self.tensor_parallel_size = tp_size
+        self.all_reduce_max = None
+        if tp_size > 1:
+            # KV heads are sharded over the TP group (tri/method.py:111-122): this
+            # rank scores its own heads and the per-layer head maxima meet in one
+            # MAX all-reduce per step (tri/method.py:447-461).
+            group = tensor_parallel_group()
+            tp_rank = int(group.rank_in_group)
+            self.all_reduce_max = max_all_reducer(group.device_group)
         device = torch.device(runner.device)
         if device.type != "cuda":
             raise RuntimeError("TriAttention on MI355X requires a HIP device")
         max_len = int(self.vllm_config.model_config.max_model_len)
-        device_stats = self.calibration.to_device(self.model_shape, device)
+        device_stats = self.calibration.to_device(
+            self.model_shape, device, tensor_parallel_rank=tp_rank, tensor_parallel_size=tp_size
+        )
         self.offsets = build_geometric_offsets(max_len, device)
 
         mtp = tuple(layer for layer in layer_caches if is_mtp_cache_layer(layer.name))
@@ -137,10 +151,11 @@ class TriAttentionMethod(KVCompressionMethod):
         self.cache_block_size = int(cache.shape[1])
         if self.cache_block_size != KERNEL_BLOCK_SIZE:
             raise RuntimeError("TriAttention requires 128-token kernel cache blocks")
-        if int(cache.shape[2]) != self.model_shape.num_kv_heads:
+        local_kv_heads = self.model_shape.num_kv_heads // tp_size
+        if int(cache.shape[2]) != local_kv_heads:
             raise RuntimeError(
-                "local KV-cache head count does not match the model shape: "
-                f"expected {self.model_shape.num_kv_heads}, got {cache.shape[2]}"
+                "local KV-cache head count does not match tensor-parallel model shape: "
+                f"expected {local_kv_heads}, got {cache.shape[2]}"
             )
         queries_per_kv_head(self.model_shape)
         scoring = self.layer_caches[:: self.config.score_layer_stride]
@@ -191,16 +206,32 @@ class TriAttentionMethod(KVCompressionMethod):
             block_size=self.cache_block_size,
             budget=self.config.kv_budget,
         )
-        self.pipeline.select_step(batch)
+        self._select(batch)
         self.pipeline.compact(batch)
         return [self._result() for _ in requests]
+
+    def _select(self, batch: Batch) -> torch.Tensor:
+        if self.all_reduce_max is not None:
+            return self.pipeline.select_step_sharded(batch, self.all_reduce_max)
+        return self.pipeline.select_step(batch)
 
     def select_keep_indices(self, source_block_ids: torch.Tensor, physical_num_tokens: int, round_start: int) -> torch.Tensor:
         """Keep indices of one request without materialising (tri/method.py:297-475)."""
         if self.pipeline is None:
             raise RuntimeError("TriAttention method is not bound to KV cache")
         batch = Batch.build(self.pipeline.device, [int(physical_num_tokens)], [int(round_start)], [source_block_ids])
-        return self.pipeline.select_step(batch)[0].clone()
+        return self._select(batch)[0].clone()
+
+
+def tensor_parallel_group() -> Any:
+    """vLLM's tensor-parallel group coordinator (``rank_in_group``,
+    ``device_group``), imported only when tensor_parallel_size > 1, as the
+    reference does (tri/method.py:113-116)."""
+    try:
+        from vllm.distributed import get_tp_group
+    except ImportError as exc:
+        raise RuntimeError("tensor_parallel_size > 1 needs vLLM's tensor-parallel group (vllm.distributed)") from exc
+    return get_tp_group()
 
 
 def create_triattention_method(

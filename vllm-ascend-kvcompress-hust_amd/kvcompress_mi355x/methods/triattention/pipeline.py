@@ -266,7 +266,7 @@ class CompressionPipeline:
         self.agg = torch.empty(self.max_tokens, dtype=torch.float32, device=dev_)
         self.keep = torch.empty((self.max_seqs, self.budget), dtype=torch.int64, device=dev_)
         self.select_ws = select_workspace(self.max_seqs, self.segments, self.policy, dev_)
-        self.layer_scores = None  # [S, max_tokens] per-layer head maxima, made on first use
+        self.layer_scores = None  # flat per-layer head maxima, viewed [S, tokens]; made on first use
         shape = (s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len)
         if self.score_aggregation == "max":
             ws = _native.load().kvc_score_max_workspace_bytes(*shape, n_off)
@@ -420,11 +420,13 @@ class CompressionPipeline:
         """Per-layer head maxima over this pipeline's query heads, [S, sum N]
         (after ``score``): the tensor the reference's TP path all-reduces with
         MAX across the ranks that hold the other KV heads
-        (tri/method.py:316-322,447-461).  Rewritten by every call."""
+        (tri/method.py:316-322,447-461).  Contiguous (collectives take
+        contiguous tensors); rewritten by every call."""
         t = self.tables
         total = batch.total_tokens
-        if self.layer_scores is None or self.layer_scores.shape[1] < total:
-            self.layer_scores = torch.empty((t.n_layers, self.max_tokens), dtype=torch.float32, device=self.device)
+        if self.layer_scores is None or self.layer_scores.numel() < t.n_layers * total:
+            self.layer_scores = torch.empty(t.n_layers * max(total, self.max_tokens), dtype=torch.float32, device=self.device)
+        scores = self.layer_scores[: t.n_layers * total].view(t.n_layers, total)
         _native.call(
             "kvc_layer_head_max",
             dev.stream_handle(self.device),
@@ -441,10 +443,10 @@ class CompressionPipeline:
             batch.n_seq * self.n_heads,
             self.n_heads,
             0,
-            dev.ptr(self.layer_scores),
-            int(self.layer_scores.stride(0)),
+            dev.ptr(scores),
+            total,
         )
-        return self.layer_scores[:, :total]
+        return scores
 
     def combine_layer_scores(self, batch: Batch, layer_scores: torch.Tensor) -> None:
         """The aggregate from layer scores reduced across the TP group: layers
@@ -463,6 +465,18 @@ class CompressionPipeline:
             dev.ptr(self.agg),
         )
 
+    def select_step_sharded(self, batch: Batch, all_reduce_max) -> torch.Tensor:
+        """Score the local heads, reduce the per-layer head maxima across the
+        group with ``all_reduce_max`` and select on the shared aggregate
+        (tri/method.py:315-322,447-475): every rank gets the same keep set."""
+        self.validate(batch)
+        self.ensure_capacity(batch)
+        self.score(batch)
+        scores = self.local_layer_scores(batch)
+        all_reduce_max(scores)
+        self.combine_layer_scores(batch, scores)
+        return self.select(batch)
+
     def step_sharded(self, batch: Batch, all_reduce_max, *, rewrite: bool = True):
         """The step of one tensor-parallel rank whose caches and calibration
         tables hold a shard of the KV heads: score the local heads, reduce the
@@ -471,13 +485,7 @@ class CompressionPipeline:
         ReduceOp.MAX on a RCCL group; the library itself issues no collective),
         then select on the shared aggregate and compact the local heads.  Every
         rank of the group gets the same keep indices."""
-        self.validate(batch)
-        self.ensure_capacity(batch)
-        self.score(batch)
-        scores = self.local_layer_scores(batch)
-        all_reduce_max(scores)
-        self.combine_layer_scores(batch, scores)
-        keep = self.select(batch)
+        keep = self.select_step_sharded(batch, all_reduce_max)
         self.compact(batch)
         if not rewrite:
             return keep, None, None
@@ -593,3 +601,24 @@ class StepGraph:
 
     def replay(self) -> None:
         self.graph.replay()
+
+
+def max_all_reducer(group):
+    """In-place elementwise MAX over a torch.distributed process group, the
+    collective of the reference's TP path (tri/method.py:447-453), as the
+    ``all_reduce_max`` argument of :meth:`CompressionPipeline.step_sharded`.
+    An RCCL ("nccl") group reduces the device tensor itself; gloo takes host
+    tensors, so a device tensor goes through a host copy and back."""
+    import torch.distributed as dist
+
+    host_copy = dist.get_backend(group) == "gloo"
+
+    def all_reduce_max(tensor: torch.Tensor) -> None:
+        if host_copy and tensor.device.type != "cpu":
+            host = tensor.to("cpu")
+            dist.all_reduce(host, op=dist.ReduceOp.MAX, group=group)
+            tensor.copy_(host)
+        else:
+            dist.all_reduce(tensor, op=dist.ReduceOp.MAX, group=group)
+
+    return all_reduce_max
