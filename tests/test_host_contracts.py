@@ -290,6 +290,38 @@ def test_workspace_query_and_argument_validation_without_gpu() -> None:
         _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4)
 
 
+def test_max_scorer_queries_and_validation_without_gpu() -> None:
+    """kvc_score_paged_max: workspace at least the mean scorer's (kvc_head_stats
+    reads its partial sums in place), and its argument checks, which run
+    before anything touches a device."""
+    from kvcompress_mi355x import _native
+
+    lib = _native.load()
+    shape = (6, 8, 128, 128, 5, 16, 16384)
+    mean_ws = lib.kvc_score_workspace_bytes(*shape)
+    assert lib.kvc_score_max_workspace_bytes(*shape, 16) > mean_ws
+    assert lib.kvc_score_max_workspace_bytes(*shape, 18) > lib.kvc_score_max_workspace_bytes(*shape, 16)
+    assert lib.kvc_score_max_workspace_bytes(*shape, 0) == 0
+    fake = 4096  # non-null placeholders; every check below fails before a dereference
+    ws = lib.kvc_score_max_workspace_bytes(*shape, 33)
+
+    def call(n_offsets, head_dim=128, rotary=128, dtype=0, workspace_bytes=ws):
+        return lib.kvc_score_paged_max(
+            None, dtype, 6, fake, 100, 128 * 8 * head_dim, 8, head_dim, rotary, 5, 0, 16, 16384, fake, fake, fake,
+            fake, fake, fake, fake, fake, fake, fake, fake, n_offsets, 0, fake, 0, 1, 16384, fake, workspace_bytes,
+        )
+
+    assert call(0) == _native.EINVAL
+    assert "n_offsets" in lib.kvc_last_error().decode()
+    assert call(33) == _native.EINVAL
+    assert "32 offsets" in lib.kvc_last_error().decode()
+    assert call(16, head_dim=96, rotary=96) == _native.EINVAL  # F = 48: not a matrix-core shape
+    assert "matrix-core" in lib.kvc_last_error().decode()
+    assert call(16, dtype=2) == _native.EINVAL  # float32 caches are not scored
+    assert call(16, workspace_bytes=mean_ws) == _native.EINVAL
+    assert "workspace too small" in lib.kvc_last_error().decode()
+
+
 def test_raw_layout_names_the_scorer_without_gpu() -> None:
     """Matrix-core shapes (bf16 or fp16, half or interleaved RoPE, head_dim and
     F multiples of 32, qpk <= 8) get head-major raw scores; the rest token-major."""
