@@ -74,7 +74,13 @@ def parse_args() -> argparse.Namespace:
         help="aggregation of the rotary score over the future offsets (the reference's score_aggregation option)",
     )
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument(
+        "--cpu-repeats",
+        type=int,
+        default=12,
+        help="timed repetitions of the CPU baseline's one-sequence sample after one warm-up (about 10 s of host "
+        "work on the default workload)",
+    )
     p.add_argument(
         "--calibrate-copy-mib",
         type=int,
