@@ -12,6 +12,8 @@ pytestmark = pytest.mark.gpu
 SPECS = {
     "private": (2, dict(n_layers=4, score_layer_stride=2, seq_lens=(3000, 1500, 4096), budget=1024, recent=64, max_model_len=8192)),
     "inplace": (4, dict(n_layers=2, score_layer_stride=1, seq_lens=(6000, 9000), pool_pages=160, max_model_len=16384)),
+    # score_aggregation="max": per-offset phase table, both folds and the max scorer in the graph.
+    "private-max": (2, dict(n_layers=4, score_layer_stride=2, seq_lens=(3000, 4096), budget=1024, recent=64, max_model_len=131072)),
 }
 
 
@@ -23,7 +25,7 @@ def test_graph_replays_match_eager_steps(hip_device, mode) -> None:
     spec = workloads.config_spec(index, **overrides)
     assert spec.inplace == (mode == "inplace")
     cache = workloads.build_synthetic_cache(spec, hip_device, seed=3)
-    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline, batch = workloads.build_pipeline(cache, score_aggregation="max" if mode.endswith("-max") else "mean")
     pristine_k = [k.clone() for k in cache.k_caches]
     pristine_v = [v.clone() for v in cache.v_caches]
     g = torch.Generator(device=hip_device).manual_seed(11)
