@@ -126,7 +126,7 @@ def test_score_paged_fp16_ranges(hip_device, case) -> None:
     assert_scores_close(out.cpu().reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
 
 
-@pytest.mark.parametrize("case", SCORE_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5])[-4:]}t{c[6]}" for c in SCORE_CASES])
+@pytest.mark.parametrize("case", SCORE_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5]).split(".")[-1]}t{c[6]}" for c in SCORE_CASES])
 def test_score_paged_matches_oracle(hip_device, case) -> None:
     kernels, _, _ = _kvc()
     kv, qpk, head_dim, rotary, style, dtype, tokens = case
@@ -183,7 +183,7 @@ MAX_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", MAX_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5])[-4:]}t{c[6]}o{c[7]}" for c in MAX_CASES])
+@pytest.mark.parametrize("case", MAX_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5]).split(".")[-1]}t{c[6]}o{c[7]}" for c in MAX_CASES])
 def test_score_paged_max_matches_oracle(hip_device, case) -> None:
     # score_aggregation="max" (tri/scoring.py:84-97) against the oracle's torch program.
     kernels, _, _ = _kvc()
@@ -214,6 +214,37 @@ def test_score_paged_max_matches_oracle(hip_device, case) -> None:
     # The maximum is not the mean: the two aggregations differ on these inputs.
     mean = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets)
     assert float((want - mean).abs().max()) > 1e-2
+
+
+@pytest.mark.parametrize("case", FP16_RANGE_CASES, ids=[f"k{c[0]:g}w{min(c[1]):g}-{max(c[1]):g}" for c in FP16_RANGE_CASES])
+def test_score_paged_max_fp16_ranges(hip_device, case) -> None:
+    # fp16 keys up to +-65000 (|k| past fp16's range) and query heads whose
+    # weights differ by 10^8: one power-of-two scale per query head for the
+    # per-offset weights, as for the mean scorer.
+    kernels, _, _ = _kvc()
+    key_scale, head_scales = case
+    kv, qpk, head_dim, tokens = 8, 5, 128, 600
+    g = torch.Generator().manual_seed(len(FP16_RANGE_CASES) + tokens + 1)
+    stats = _random_stats(g, kv, qpk, head_dim // 2, 0, head_dim)
+    w = torch.tensor(head_scales, dtype=torch.float32).view(1, qpk, 1)
+    stats = ref.LayerStats(stats.q_mean_real, stats.q_mean_imag, stats.q_abs_mean, stats.freq_scale_sq * w.square(), stats.omega,
+                           stats.rope_style, stats.rotary_dim, stats.q_pass_mean)
+    n_blocks = -(-tokens // 128)
+    pool = n_blocks + 3
+    cache = (torch.randn(pool, 128, kv, head_dim, generator=g) * key_scale).clamp(-65000.0, 65000.0).to(torch.float16)
+    blocks = torch.randperm(pool, generator=g)[:n_blocks]
+    offsets = ref.build_geometric_offsets(131072)
+    round_start = tokens + 5
+    keys = ref.gather_paged_range(cache, blocks, start=0, count=tokens, block_size=128)
+    want = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets, aggregation="max")
+    out = torch.full((kv, qpk, tokens), float("nan"), device=hip_device)
+    d = lambda t: t.to(hip_device)  # noqa: E731
+    assert kernels.score_paged_keys_max(
+        d(cache), d(blocks), d(stats.q_mean_real), d(stats.q_mean_imag), d(torch.sqrt(stats.freq_scale_sq)),
+        d(stats.q_abs_mean - torch.sqrt(stats.q_mean_real.square() + stats.q_mean_imag.square() + 1e-8)),
+        d(stats.omega), d(offsets), round_start, tokens, out, 128, "half",
+    )
+    assert_scores_close(out.cpu().reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
 
 
 def test_score_paged_max_nan_key(hip_device) -> None:
