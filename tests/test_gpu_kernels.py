@@ -126,7 +126,7 @@ def test_score_paged_fp16_ranges(hip_device, case) -> None:
     assert_scores_close(out.cpu().reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
 
 
-@pytest.mark.parametrize("case", SCORE_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5]).split(".")[-1]}t{c[6]}" for c in SCORE_CASES])
+@pytest.mark.parametrize("case", SCORE_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5]).split('.')[-1]}t{c[6]}" for c in SCORE_CASES])
 def test_score_paged_matches_oracle(hip_device, case) -> None:
     kernels, _, _ = _kvc()
     kv, qpk, head_dim, rotary, style, dtype, tokens = case
@@ -183,7 +183,7 @@ MAX_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", MAX_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5]).split(".")[-1]}t{c[6]}o{c[7]}" for c in MAX_CASES])
+@pytest.mark.parametrize("case", MAX_CASES, ids=[f"kv{c[0]}q{c[1]}d{c[2]}r{c[3]}{c[4][0]}{str(c[5]).split('.')[-1]}t{c[6]}o{c[7]}" for c in MAX_CASES])
 def test_score_paged_max_matches_oracle(hip_device, case) -> None:
     # score_aggregation="max" (tri/scoring.py:84-97) against the oracle's torch program.
     kernels, _, _ = _kvc()
