@@ -138,7 +138,7 @@ def _oracle_sequence(cache, spec, pipeline, batch, b: int, host_keys) -> int:
     stats = cache.calibration.to_device(spec.model_shape(), torch.device("cpu"))
     cfg = ref.MethodConfig(
         budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
-        score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
+        score_aggregation=pipeline.score_aggregation, score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
     )
     n = spec.seq_lens[b]
     out = ref.method_select(
@@ -169,7 +169,7 @@ def _oracle_sequence(cache, spec, pipeline, batch, b: int, host_keys) -> int:
     return assert_keep_matches(pipeline.keep[b], out["keep"], out["agg"], spec.budget, protected)
 
 
-def _run_full(spec, hip_device, oracle_seqs) -> None:
+def _run_full(spec, hip_device, oracle_seqs, score_aggregation: str = "mean") -> None:
     from kvcompress_mi355x import workloads
 
     gc.collect()
@@ -177,7 +177,7 @@ def _run_full(spec, hip_device, oracle_seqs) -> None:
     print(f"full-size workload {spec.name}: {len(spec.seq_lens)} sequences, {spec.total_tokens} tokens, "
           f"{spec.n_layers} layers", flush=True)
     cache = workloads.build_synthetic_cache(spec, hip_device, seed=0)
-    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline, batch = workloads.build_pipeline(cache, score_aggregation=score_aggregation)
     keep = pipeline.select_step(batch)
     host_keys = {b: _host_keys(cache, spec, b) for b in oracle_seqs}
     snapshot = _front_snapshot(cache, spec) if spec.inplace else None
@@ -219,3 +219,13 @@ def test_fullsize_decode_batch_fp16(hip_device) -> None:
     # Every triggered sequence at its full length; 12 of the 24 benchmark
     # layers materialised (two scoring layers) to leave room for the checks.
     _run_full(workloads.config_spec(5, n_layers=12), hip_device, oracle_seqs=(0,))
+
+
+def test_fullsize_qwen3_5_hybrid_score_max(hip_device) -> None:
+    from kvcompress_mi355x import workloads
+
+    # score_aggregation="max" (19 offsets); the oracle's per-offset torch loop
+    # runs on the shortest sequence.
+    spec = workloads.config_spec(3)
+    shortest = min(range(len(spec.seq_lens)), key=lambda i: spec.seq_lens[i])
+    _run_full(spec, hip_device, oracle_seqs=(shortest,), score_aggregation="max")
