@@ -1,7 +1,7 @@
 """CPU oracle of the TriAttention compression path -- TEST INFRASTRUCTURE ONLY.
 
 Nothing in the product imports this package.  It is used by tests/, by
-__graft_entry__.smoke() as the checker, and by bench.py's cpu_baseline leg as
+__graft_entry__.smoke() to verify its result, and by bench.py's cpu_baseline leg as
 the timed CPU baseline ("port" kind).
 
 Modules

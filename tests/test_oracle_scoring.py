@@ -1,5 +1,5 @@
 """Pin the oracle's scorer: reference known-answer tests, closed forms and a
-float64 brute force (the oracle is the checker for the HIP scorer)."""
+float64 brute force (the HIP scorer's parity tests compare against this oracle)."""
 
 from __future__ import annotations
 

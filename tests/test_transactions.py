@@ -1,6 +1,6 @@
 """Scheduler and worker halves of the compression transaction protocol, with
 the scenarios of the reference's scheduler tests (tests/test_stateful.py:
-404-506, 855-915, 559-583) restated on this build's host-agnostic API: one
+404-506, 855-915, 559-583) restated on the host-agnostic API here: one
 request "r" of 300 prompt tokens in blocks [3, 4, 5], budget 128 and recompute
 window 128 (threshold 256), destination blocks taken from a pool starting at
 50."""

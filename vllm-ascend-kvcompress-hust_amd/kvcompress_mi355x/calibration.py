@@ -632,7 +632,7 @@ def _load_calibration_text(request: CalibrationRequest) -> tuple[str, str]:
 
 def _prepare_device(device: str) -> None:
     if str(device).startswith("npu"):
-        raise RuntimeError("this build calibrates on HIP devices ('cuda' in torch); 'npu' is not available")
+        raise RuntimeError("calibration runs on HIP devices ('cuda' in torch); 'npu' is not available")
 
 
 def _empty_device_cache(device: str, *, all_devices: bool = False) -> None:
