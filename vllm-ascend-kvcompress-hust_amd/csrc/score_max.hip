@@ -139,6 +139,43 @@ __device__ __attribute__((aligned(16))) uint32_t kZeroKeys[8 * 16];
 // (one v_maximum3_f32 on gfx950).
 __device__ __forceinline__ float max_prop(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
+// bf16 fragments need no per-column scale: one thread per (column, chunk and
+// step, operand lane) writes that lane's hi and lo words.
+__global__ __launch_bounds__(256) void fold_offsets_bf16_kernel(OffsetFoldArgs m) {
+  typedef MfmaElem<false> E;
+  const FoldArgs& a = m.f;
+  const int n_pos = m.nch * m.nr;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t cols = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * a.qpk;
+  if (idx >= cols * n_pos * 64) return;
+  const int lane = static_cast<int>(idx & 63);
+  const int p = static_cast<int>((idx >> 6) % n_pos);
+  const int64_t col = (idx >> 6) / n_pos;
+  const int g = static_cast<int>(col % a.qpk);
+  int64_t r = col / a.qpk;
+  const int head = static_cast<int>(r % a.kv_heads);
+  r /= a.kv_heads;
+  const int layer = static_cast<int>(r % a.n_layers);
+  const int b = static_cast<int>(r / a.n_layers);
+  const int64_t row = (static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + g;
+  const int j = lane & 15, kb = lane >> 4;
+  const int c = p / m.nr, st = p - c * m.nr;
+  const int o = min(16 * c + j, m.n_offsets - 1);
+  u32x4 hi, lo;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float v0 = offset_weight(a, b, layer, row, o, m.n_offsets, 32 * st + 8 * kb + 2 * w);
+    const float v1 = offset_weight(a, b, layer, row, o, m.n_offsets, 32 * st + 8 * kb + 2 * w + 1);
+    const uint32_t h = E::pack(v0, v1);
+    hi[w] = h;
+    lo[w] = E::pack(v0 - E::lo(h), v1 - E::hi(h));
+  }
+  u32x4* dst = m.frags + (col * n_pos * 2 + 2 * p) * 64 + lane;
+  dst[0] = hi;
+  dst[64] = lo;
+  if (p == 0 && lane == 0) m.inv_scale[col] = 1.0f;
+}
+
 struct MaxGeometry {
   int gpg;     // query heads per workgroup
   int groups;  // query-head groups per KV head
@@ -540,7 +577,7 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   if (f16)
     fold_offsets_kernel<true><<<static_cast<unsigned>(ceil_div(cols, 4)), 256, 0, stream>>>(m);
   else
-    fold_offsets_kernel<false><<<static_cast<unsigned>(ceil_div(cols, 4)), 256, 0, stream>>>(m);
+    fold_offsets_bf16_kernel<<<static_cast<unsigned>(ceil_div(cols * geo.nch * nr * 64, 256)), 256, 0, stream>>>(m);
   if (int rc = launch_status("kvc_score_paged_max(fold)")) return rc;
 
   const float* rest_scale =
