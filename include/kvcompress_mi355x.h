@@ -150,10 +150,12 @@ size_t kvc_score_max_workspace_bytes(int n_layers, int kv_heads, int head_dim, i
  *                           + sum_f a*extra*|k_f| + sum_p q_pass*k_pass
  * Arguments as kvc_score_paged except offset_cos/offset_sin: the
  * kvc_offset_phases tables [n_seq][n_layers][n_offsets][F], sequence stride
- * phase_seq_stride elements (0 = one table shared by all sequences).  Served
- * for the matrix-core shapes only (bf16 or fp16, head_dim 64, 128 or 256,
- * rotary_dim/2 a multiple of 32); KVC_EINVAL otherwise.  Partial sums for
- * kvc_head_stats land where kvc_score_paged leaves them. */
+ * phase_seq_stride elements (0 = one table shared by all sequences), at most
+ * 32 offsets.  Shapes as kvc_score_paged (bf16 or fp16); the matrix-core
+ * scorer serves head_dim 64, 128 or 256 with rotary_dim/2 a multiple of 32, a
+ * vector-ALU scorer the rest (KVC_EINVAL when one query head's per-offset
+ * weights exceed 64 KB of LDS).  Partial sums for kvc_head_stats land where
+ * kvc_score_paged leaves them. */
 int kvc_score_paged_max(kvc_stream_t stream, int dtype, int n_layers, const uint64_t* k_layer_ptrs,
                         int64_t num_pages, int64_t page_stride, int kv_heads, int head_dim,
                         int rotary_dim, int qpk, int rope_style, int n_seq, int max_seq_len,

@@ -180,6 +180,11 @@ MAX_CASES = [
     (2, 8, 256, 64, "interleaved", torch.float16, 300, 32768),
     (2, 4, 64, 64, "half", torch.bfloat16, 257, 8),               # 4 offsets
     (1, 8, 256, 256, "half", torch.bfloat16, 130, 65536),         # F = 128: one query head per workgroup
+    # vector-ALU path: F not a multiple of 32 or head_dim not 64/128/256
+    (4, 4, 128, 32, "half", torch.bfloat16, 400, 32768),          # F = 16, partial RoPE
+    (2, 6, 96, 96, "interleaved", torch.float16, 350, 131072),    # F = 48, 18 offsets
+    (2, 2, 80, 80, "half", torch.bfloat16, 300, 16384),           # head_dim 80
+    (2, 3, 192, 64, "interleaved", torch.bfloat16, 600, 262144),  # head_dim 192, partial RoPE, 19 offsets
 ]
 
 

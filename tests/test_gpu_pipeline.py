@@ -155,6 +155,20 @@ def test_score_aggregation_max(hip_device, config, overrides, layer_aggregation)
     assert near <= 4
 
 
+@pytest.mark.parametrize("score_aggregation", ["mean", "max"])
+def test_vector_alu_scorer_shape(hip_device, score_aggregation) -> None:
+    # head_dim 96 (F = 48): the vector-ALU scorers and token-major raw scores.
+    from kvcompress_mi355x import _native, workloads
+
+    spec = workloads.config_spec(
+        2, n_layers=2, score_layer_stride=1, seq_lens=(3000, 4500), budget=1024, recent=64, head_dim=96, rotary_dim=96,
+        num_attention_heads=12, num_kv_heads=4, max_model_len=65536,
+    )
+    assert _native.load().kvc_score_raw_layout(0, 0, 4, 96, 96, 3) == _native.RAW_TOKEN_MAJOR
+    _, _, _, near = _run_and_check(spec, hip_device, score_aggregation=score_aggregation)
+    assert near <= 4
+
+
 def test_fp16_decode_shape(hip_device) -> None:
     from kvcompress_mi355x import workloads
 

@@ -305,9 +305,9 @@ def test_max_scorer_queries_and_validation_without_gpu() -> None:
     fake = 4096  # non-null placeholders; every check below fails before a dereference
     ws = lib.kvc_score_max_workspace_bytes(*shape, 33)
 
-    def call(n_offsets, head_dim=128, rotary=128, dtype=0, workspace_bytes=ws):
+    def call(n_offsets, head_dim=128, rotary=128, dtype=0, workspace_bytes=ws, kv=8):
         return lib.kvc_score_paged_max(
-            None, dtype, 6, fake, 100, 128 * 8 * head_dim, 8, head_dim, rotary, 5, 0, 16, 16384, fake, fake, fake,
+            None, dtype, 6, fake, 100, 128 * kv * head_dim, kv, head_dim, rotary, 5, 0, 16, 16384, fake, fake, fake,
             fake, fake, fake, fake, fake, fake, fake, fake, n_offsets, 0, fake, 0, 1, 16384, fake, workspace_bytes,
         )
 
@@ -315,8 +315,11 @@ def test_max_scorer_queries_and_validation_without_gpu() -> None:
     assert "n_offsets" in lib.kvc_last_error().decode()
     assert call(33) == _native.EINVAL
     assert "32 offsets" in lib.kvc_last_error().decode()
-    assert call(16, head_dim=96, rotary=96) == _native.EINVAL  # F = 48: not a matrix-core shape
-    assert "matrix-core" in lib.kvc_last_error().decode()
+    # The vector-ALU path keeps every offset's weights of one query head in LDS:
+    # 32 offsets x 256 frequencies do not fit.
+    big = lib.kvc_score_max_workspace_bytes(6, 1, 512, 512, 5, 16, 16384, 32)
+    assert call(32, head_dim=512, rotary=512, kv=1, workspace_bytes=big) == _native.EINVAL
+    assert "LDS" in lib.kvc_last_error().decode()
     assert call(16, dtype=2) == _native.EINVAL  # float32 caches are not scored
     assert call(16, workspace_bytes=mean_ws) == _native.EINVAL
     assert "workspace too small" in lib.kvc_last_error().decode()

@@ -829,10 +829,6 @@ extern "C" int kvc_score_paged_max(kvc_stream_t stream, int dtype, int n_layers,
                            offset_sin, phase_seq_stride, raw, raw_layer_stride, raw_token_stride, raw_head_stride,
                            workspace, workspace_bytes_given, need, &s, &fa, &sa))
     return rc;
-  if (!mfma_scorer_supported(s, dtype, rope_style))
-    return fail(KVC_EINVAL,
-                "kvc_score_paged_max: the max-over-offsets scorer needs the matrix-core shape "
-                "(head_dim 64, 128 or 256 and rotary_dim/2 a multiple of 32)");
   if (phase_seq_stride != 0 && phase_seq_stride < static_cast<int64_t>(n_layers) * n_offsets * s.freq)
     return fail(KVC_EINVAL, "kvc_score_paged_max: phase_seq_stride smaller than one sequence's table");
   if (s.max_tiles == 0) return 0;

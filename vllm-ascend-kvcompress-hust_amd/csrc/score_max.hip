@@ -513,6 +513,149 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
   }
 }
 
+// ------------------------------------------------------- vector-ALU path --
+
+// Shapes the matrix-core scorer does not serve (F not a multiple of 32, or
+// head_dim other than 64/128/256): one thread per token of a 256-token span
+// for one query head.  The workgroup folds that head's per-offset weights
+// (real / imaginary part per frequency, rows past the last offset repeating
+// it) and its magnitude and pass weights into LDS, then each thread walks its
+// key row in blocks of 8 frequencies (16-byte loads of the real and the
+// imaginary parts), accumulating 16*NCH offset sums, the magnitude term and
+// the pass term; LDS weight reads are wave-wide broadcasts.
+constexpr int kValuMaxLds = 64 * 1024;
+
+template <typename Tag, bool IL, int NCH>
+__global__ __launch_bounds__(256) void score_max_valu_kernel(ScoreArgs a, FoldArgs f, int qpk, int n_offsets) {
+  constexpr int OO = 16 * NCH;
+  extern __shared__ __attribute__((aligned(16))) float lds_w[];  // wre[OO][F], wim[OO][F], wm[F], wp[P]
+  const int F = a.freq, P = a.head_dim - a.rotary_dim;
+  float* wre = lds_w;
+  float* wim = wre + OO * F;
+  float* wm = wim + OO * F;
+  float* wp = wm + F;
+  const int n_heads = a.kv_heads * qpk;
+  const int q = blockIdx.z % n_heads;
+  const int layer = blockIdx.z / n_heads;
+  const int b = blockIdx.y;
+  const int tile = blockIdx.x;
+  const int n = a.seq_lens[b];
+  const int t0 = tile * kScoreTile;
+  if (t0 >= n) return;  // whole workgroup
+  const int head = q / qpk, g = q - head * qpk;
+  const int64_t row = (static_cast<int64_t>(layer) * a.kv_heads + head) * qpk + g;
+
+  for (int i = threadIdx.x; i < OO * F; i += blockDim.x) {
+    const int o = min(i / F, n_offsets - 1), fr = i - (i / F) * F;
+    const int64_t ph = b * f.phase_seq_stride + (static_cast<int64_t>(layer) * n_offsets + o) * F + fr;
+    const int64_t qi_ = row * F + fr;
+    const float qr = f.q_real[qi_], qi = f.q_imag[qi_], sc = f.scale[qi_];
+    const float c = f.phase_cos[ph], sn = f.phase_sin[ph];
+    wre[i] = sc * (qr * c - qi * sn);
+    wim[i] = sc * (qi * c + qr * sn);
+  }
+  for (int i = threadIdx.x; i < F; i += blockDim.x) wm[i] = f.scale[row * F + i] * f.extra[row * F + i];
+  for (int i = threadIdx.x; i < P; i += blockDim.x) wp[i] = f.q_pass[row * P + i];
+  __syncthreads();
+
+  const int t = t0 + threadIdx.x;
+  const bool valid = t < n;
+  KVC_GLOBAL const uint16_t* kbase = gptr_from_int<const uint16_t>(a.k_layer_ptrs[layer]);
+  const int64_t* bt = a.block_ids + a.block_offsets[b];
+  const int64_t n_blocks = a.block_offsets[b + 1] - a.block_offsets[b];
+  const int64_t blk = valid ? (t >> kBlockShift) : 0;
+  const int64_t page = blk < n_blocks ? bt[blk] : -1;
+  const bool page_ok = valid && page >= 0 && page < a.num_pages;
+  KVC_GLOBAL const uint16_t* krow =
+      kbase + (page_ok ? page : 0) * a.page_stride +
+      static_cast<int64_t>(t & (kBlockSize - 1)) * a.kv_heads * a.head_dim + static_cast<int64_t>(head) * a.head_dim;
+
+  float acc[OO];
+#pragma unroll
+  for (int o = 0; o < OO; ++o) acc[o] = 0.0f;
+  float mag = 0.0f, pass = 0.0f;
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  for (int fb = 0; fb < F; fb += 8) {
+    u32x4_t va = {0, 0, 0, 0}, vb = {0, 0, 0, 0};
+    if (page_ok) {
+      va = *reinterpret_cast<KVC_GLOBAL const u32x4_t*>(krow + (IL ? 2 * fb : fb));
+      vb = *reinterpret_cast<KVC_GLOBAL const u32x4_t*>(krow + (IL ? 2 * fb + 8 : F + fb));
+    }
+    float re[8], im[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (IL) {  // (re, im) pairs: va holds frequencies fb..fb+3, vb fb+4..fb+7
+        re[j] = Unpack<Tag>::lo(va[j]);
+        im[j] = Unpack<Tag>::hi(va[j]);
+        re[4 + j] = Unpack<Tag>::lo(vb[j]);
+        im[4 + j] = Unpack<Tag>::hi(vb[j]);
+      } else {
+        re[2 * j] = Unpack<Tag>::lo(va[j]);
+        re[2 * j + 1] = Unpack<Tag>::hi(va[j]);
+        im[2 * j] = Unpack<Tag>::lo(vb[j]);
+        im[2 * j + 1] = Unpack<Tag>::hi(vb[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mag = fmaf(wm[fb + j], __builtin_amdgcn_sqrtf(fmaf(im[j], im[j], re[j] * re[j])), mag);
+#pragma unroll
+    for (int o = 0; o < OO; ++o) {
+      const float* r_ = wre + o * F + fb;
+      const float* i_ = wim + o * F + fb;
+      float v = acc[o];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v = fmaf(r_[j], re[j], fmaf(i_[j], im[j], v));
+      acc[o] = v;
+    }
+  }
+  for (int pb = 0; pb < P; pb += 8) {
+    u32x4_t v = {0, 0, 0, 0};
+    if (page_ok) v = *reinterpret_cast<KVC_GLOBAL const u32x4_t*>(krow + a.rotary_dim + pb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pass = fmaf(wp[pb + 2 * j], Unpack<Tag>::lo(v[j]), pass);
+      pass = fmaf(wp[pb + 2 * j + 1], Unpack<Tag>::hi(v[j]), pass);
+    }
+  }
+  float best = acc[0];
+#pragma unroll
+  for (int o = 1; o < OO; ++o) best = max_prop(best, acc[o]);
+  const float score = best + mag + pass;
+
+  double s0 = 0.0, s1 = 0.0;
+  if (valid) {
+    a.raw[layer * a.raw_layer_stride + (a.token_offsets[b] + t) * a.raw_token_stride + q * a.raw_head_stride] = score;
+    s0 = static_cast<double>(score);
+    s1 = s0 * s0;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    s0 += __shfl_xor(s0, off);
+    s1 += __shfl_xor(s1, off);
+  }
+  __shared__ double red[2][4];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][wave] = s0;
+    red[1][wave] = s1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double* dst = a.partials + (((static_cast<int64_t>(layer) * a.n_seq + b) * a.max_tiles + tile) * n_heads + q) * 2;
+    dst[0] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    dst[1] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  }
+}
+
+using ValuMaxKernel = void (*)(ScoreArgs, FoldArgs, int, int);
+
+template <typename Tag, bool IL>
+ValuMaxKernel pick_valu_max(int nch) {
+  if (nch == 1) return score_max_valu_kernel<Tag, IL, 1>;
+  if (nch == 2) return score_max_valu_kernel<Tag, IL, 2>;
+  return nullptr;
+}
+
 using MaxKernel = void (*)(ScoreArgs, MaxGeometry, int, const u32x4*, const float*, const u32x4*, const float*);
 
 template <int NCH, bool F16, bool IL>
@@ -546,6 +689,19 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   if (geo.nch > 2)
     return fail(KVC_EINVAL, "kvc_score_paged_max: at most 32 offsets (got %d; 2^0 .. 2^30 are 31)", n_offsets);
   const int nch = geo.nch;
+  if (!mfma_scorer_supported(s, dtype, fa.interleaved ? KVC_ROPE_INTERLEAVED : KVC_ROPE_HALF)) {
+    const size_t lds = sizeof(float) * (2 * static_cast<size_t>(16 * nch) * s.freq + s.freq + s.pass);
+    if (lds > static_cast<size_t>(kValuMaxLds))
+      return fail(KVC_EINVAL, "kvc_score_paged_max: %d offsets x %d frequencies exceed the LDS of one workgroup",
+                  n_offsets, s.freq);
+    const int64_t gz = static_cast<int64_t>(s.n_layers) * s.kv_heads * s.qpk;
+    if (gz > 65535) return fail(KVC_EINVAL, "kvc_score_paged_max: too many layers x query heads for one launch");
+    ValuMaxKernel vk = f16 ? (fa.interleaved ? pick_valu_max<Fp16Tag, true>(nch) : pick_valu_max<Fp16Tag, false>(nch))
+                           : (fa.interleaved ? pick_valu_max<Bf16Tag, true>(nch) : pick_valu_max<Bf16Tag, false>(nch));
+    dim3 grid(static_cast<unsigned>(s.max_tiles), static_cast<unsigned>(s.n_seq), static_cast<unsigned>(gz));
+    vk<<<grid, 256, lds, stream>>>(sa, fa, s.qpk, n_offsets);
+    return launch_status("kvc_score_paged_max");
+  }
   MaxKernel kern = f16 ? (fa.interleaved ? pick_max_typed<true, true>(nk, nf, nch) : pick_max_typed<true, false>(nk, nf, nch))
                        : (fa.interleaved ? pick_max_typed<false, true>(nk, nf, nch) : pick_max_typed<false, false>(nk, nf, nch));
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged_max: no scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);

@@ -250,11 +250,6 @@ class CompressionPipeline:
         if layout < 0:
             _native.check(layout, "kvc_score_raw_layout")
         self.head_major = layout == _native.RAW_HEAD_MAJOR
-        if self.score_aggregation == "max" and not self.head_major:
-            raise ValueError(
-                "score_aggregation 'max' runs on the matrix-core scorer: bf16 or fp16 caches, head_dim 64, 128 or 256 "
-                "and rotary_dim/2 a multiple of 32"
-            )
         if self.head_major:
             # Token axis padded to 64 so every head row starts 256-byte aligned.
             padded = -(-self.max_tokens // 64) * 64
