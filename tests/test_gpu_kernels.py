@@ -699,3 +699,49 @@ def test_shift_seq_lens_matches_oracle(hip_device, dtype) -> None:
     dev_lens = lens.to(hip_device)
     kernels.shift_seq_lens(dev_lens, off.to(hip_device), 2)
     assert dev_lens.cpu().tolist() == ref.physical_seq_lens(lens, off, 2).tolist() == [129, 21, 50]
+
+
+@pytest.mark.parametrize("aggregation", ["mean", "max"])
+@pytest.mark.parametrize(
+    ("kv", "qpk", "head_dim", "rotary", "style", "tokens"),
+    [(2, 4, 128, 128, "half", 1000), (2, 8, 256, 64, "interleaved", 300), (2, 3, 96, 96, "half", 77)],
+)
+def test_score_post_rope_keys_matches_oracle(hip_device, aggregation, kv, qpk, head_dim, rotary, style, tokens) -> None:
+    # The reference's dense-key scoring function (tri/scoring.py:23-120) under
+    # its own name, on the HIP scorers.
+    from kvcompress_mi355x.methods.triattention import scoring
+    from kvcompress_mi355x.methods.triattention.stats import DeviceLayerCalibrationStats
+
+    g = torch.Generator().manual_seed(kv * 100 + head_dim + tokens)
+    stats = _random_stats(g, kv, qpk, rotary // 2, head_dim - rotary, rotary, style=style)
+    keys = torch.randn(tokens, kv, head_dim, generator=g).to(torch.bfloat16)
+    offsets = ref.build_geometric_offsets(65536)
+    want = ref.score_post_rope_keys(keys, stats, round_start=tokens + 9, offsets=offsets, aggregation=aggregation)
+    d = lambda t: None if t is None else t.to(hip_device)  # noqa: E731
+    dstats = DeviceLayerCalibrationStats(
+        d(stats.q_mean_real), d(stats.q_mean_imag), d(stats.q_abs_mean), d(stats.freq_scale_sq), d(stats.omega),
+        style, None if rotary == head_dim else rotary, d(stats.q_pass_mean),
+    )
+    got = scoring.score_post_rope_keys(d(keys), dstats, round_start=tokens + 9, offsets=d(offsets), aggregation=aggregation)
+    assert got.shape == want.shape
+    assert_scores_close(got.cpu().reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
+    with pytest.raises(ValueError, match="unsupported score aggregation"):
+        scoring.score_post_rope_keys(d(keys), dstats, round_start=1, offsets=d(offsets), aggregation="median")
+
+
+def test_gather_paged_range_matches_oracle(hip_device) -> None:
+    from kvcompress_mi355x.methods.triattention import cache as kcache
+
+    g = torch.Generator().manual_seed(8)
+    pool = torch.randn(6, 128, 2, 64, generator=g).to(torch.bfloat16)
+    blocks = torch.tensor([4, 1, 5])
+    want = ref.gather_paged_range(pool, blocks, start=100, count=200, block_size=128)
+    got = kcache.gather_paged_range(pool.to(hip_device), blocks.to(hip_device), start=100, count=200, block_size=128)
+    assert torch.equal(got.cpu(), want)
+    # Padded pages (page stride past the page's elements), as the reference's
+    # interleaved K/V storage has (tests/test_cache.py:50-94).
+    padded = torch.zeros(6, 2, 128, 2, 64, dtype=torch.bfloat16)
+    padded[:, 0] = pool
+    k_view = padded.to(hip_device)[:, 0]
+    got = kcache.gather_paged_range(k_view, blocks.to(hip_device), start=0, count=384, block_size=128)
+    assert torch.equal(got.cpu(), ref.gather_paged_range(pool, blocks, start=0, count=384, block_size=128))

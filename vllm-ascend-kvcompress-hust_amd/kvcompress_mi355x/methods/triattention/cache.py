@@ -1,7 +1,8 @@
 """Paged-cache slot arithmetic and K/V materialisation on the GPU (tri/cache.py).
 
-``token_slots`` and ``materialize_token_slots`` keep the reference names and
-contracts (tri/cache.py:9-15,100-112); ``materialize_selected_tokens`` keeps
+``token_slots``, ``gather_paged_tokens`` / ``gather_paged_range`` and
+``materialize_token_slots`` keep the reference names and contracts
+(tri/cache.py:9-15,48-76,100-112); ``materialize_selected_tokens`` keeps
 tri/cache.py:79-97.  The fast path used by the compression step is
 ``compact_layers``: one launch moves the kept rows of every layer.
 """
@@ -34,6 +35,28 @@ def token_slots(block_ids: torch.Tensor, token_indices: torch.Tensor, block_size
         dev.ptr(out),
     )
     return out
+
+
+def gather_paged_tokens(
+    cache: torch.Tensor, block_ids: torch.Tensor, token_indices: torch.Tensor, block_size: int
+) -> torch.Tensor:
+    """Rows of logical tokens from ``[blocks, block, heads, dim]`` storage as a
+    dense ``[tokens, heads, dim]`` tensor (tri/cache.py:48-58).  A helper for
+    callers of the reference's torch path: the compression step reads pages in
+    its kernels and never gathers."""
+    if cache.ndim != 4 or cache.shape[1] != block_size:
+        raise ValueError("cache must use [blocks, block, heads, dim] layout")
+    dev.require_hip(cache, "cache")
+    slots = token_slots(block_ids, token_indices, block_size)
+    return cache[torch.div(slots, block_size, rounding_mode="floor"), torch.remainder(slots, block_size)]
+
+
+def gather_paged_range(
+    cache: torch.Tensor, block_ids: torch.Tensor, *, start: int, count: int, block_size: int
+) -> torch.Tensor:
+    """One contiguous logical range of tokens (tri/cache.py:61-76)."""
+    indices = torch.arange(start, start + count, device=block_ids.device, dtype=torch.long)
+    return gather_paged_tokens(cache, block_ids, indices, block_size)
 
 
 def _cache_geometry(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, int]:
