@@ -334,19 +334,25 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     for (int j = 0; j < NK; ++j) ka[j] = load_k(reinterpret_cast<KVC_GLOBAL const u32x4*>(row + 32 * j));
   };
 
-  // Wave w scores tiles (w, w+4) and (w+8, w+12) of every span; the keys of
-  // the next pair, also across a span boundary and the span's epilogue, are in
-  // flight while a pair is scored.
-  static_assert(kScoreTile == 16 * 4 * kStreams, "two pairs of tiles per wave cover a span");
+  // Wave w scores tiles w, w+4, w+8, w+12 of every span in groups of T tiles
+  // (T = 2: each fragment read feeds two tiles; T = 1 for head_dim 256,
+  // whose key registers would otherwise leave one wave per SIMD: 0.52 against
+  // 0.69 ms on the Qwen3.5 shape, while T = 2 is 6% faster at head_dim 128).
+  // The keys of the next group, also across a span boundary and the span's
+  // epilogue, are in flight while a group is scored.
+  constexpr int T = NK >= 8 ? 1 : 2;
+  constexpr int kGroups = 4 / T;
+  static_assert(kScoreTile == 16 * 4 * kStreams, "four tiles per wave cover a span");
+  static_assert(kGroups % 2 == 0, "a span's first group lands in buffer 0");
   const int n_sp = min(kMaxSpans, (n - tile_first * kScoreTile + kScoreTile - 1) / kScoreTile);
-  u32x4 ka[2][NK], kn[2][NK];
+  u32x4 kbuf[2][T][NK];
   SpanPages pages;
   pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, tile_first * kScoreTile);
   {
     const int st0 = tile_first * kScoreTile;
     const int st1 = min(n, st0 + kScoreTile);
-    load_tile(pages, st0, st1, wave, ka[0]);
-    load_tile(pages, st0, st1, wave + kStreams, ka[1]);
+#pragma unroll
+    for (int u = 0; u < T; ++u) load_tile(pages, st0, st1, wave + kStreams * u, kbuf[0][u]);
   }
   for (int sp = 0; sp < n_sp; ++sp) {
     const int tile = tile_first + sp;
@@ -363,55 +369,60 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
       for (int i = 0; i < 4; ++i) stage_rows[i][mt * 16] = v[i];
     };
 
-    // Two tiles per pass over the staged fragments.  The maximum of query
-    // head g is reduced while the MFMAs of head g + 1 run.
-    auto score_pair = [&](int mt0, const u32x4 (&k0)[NK], int mt1, const u32x4 (&k1)[NK]) {
-      const f32x4 rest0 = rest_tile(k0);
-      const f32x4 rest1 = rest_tile(k1);
-      f32x4 mx0 = {0.0f, 0.0f, 0.0f, 0.0f}, mx1 = {0.0f, 0.0f, 0.0f, 0.0f};
-      f32x4 pend0 = {0.0f, 0.0f, 0.0f, 0.0f}, pend1 = pend0;
+    // T tiles per pass over the staged fragments.  The maximum of query head
+    // g is reduced while the MFMAs of head g + 1 run.
+    auto score_group = [&](int mt_first, const u32x4 (&kk)[T][NK]) {
+      f32x4 rest[T], mx[T], pend[T], best[T];
+#pragma unroll
+      for (int u = 0; u < T; ++u) {
+        rest[u] = rest_tile(kk[u]);
+        mx[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        pend[u] = mx[u];
+      }
       int pend_g = -1;  // no lane takes head -1
       auto retire = [&]() {
-        const float v0 = token_max(pend0);
-        const float v1 = token_max(pend1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool mine = 4 * kb + i == pend_g;
-          mx0[i] = mine ? v0 : mx0[i];
-          mx1[i] = mine ? v1 : mx1[i];
+        for (int u = 0; u < T; ++u) {
+          const float v = token_max(pend[u]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx[u][i] = (4 * kb + i == pend_g) ? v : mx[u][i];
         }
       };
       // One item = one 16-offset chunk of one query head: 2*NR fragment
-      // reads and 4*NR MFMAs.  Items alternate between two register buffers
+      // reads and 2*NR*T MFMAs.  Items alternate between two register buffers
       // so the next item's fragments are read while this item's MFMAs run.
-      f32x4 best0, best1;
       auto item = [&](auto parity, int it, const vec_t (&w)[2 * NR]) {
         constexpr int P = decltype(parity)::value;
-        f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
-        f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 acc[T][2];
+#pragma unroll
+        for (int u = 0; u < T; ++u) acc[u][0] = acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < NR; ++st) {
-          const vec_t x0 = __builtin_bit_cast(vec_t, k0[st]);
-          const vec_t x1 = __builtin_bit_cast(vec_t, k1[st]);
-          acc0 = E::mfma(w[2 * st], x0, acc0);
-          acc1 = E::mfma(w[2 * st], x1, acc1);
-          acc0 = E::mfma(w[2 * st + 1], x0, acc0);
-          acc1 = E::mfma(w[2 * st + 1], x1, acc1);
-        }
-        if constexpr (NCH == 1 || P == 0) {
-          best0 = acc0;
-          best1 = acc1;
-        } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            best0[i] = max_prop(best0[i], acc0[i]);
-            best1[i] = max_prop(best1[i], acc1[i]);
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int u = 0; u < T; ++u) {
+              // T = 2: two chains (one per tile) each take hi then lo;
+              // T = 1: hi and lo go to separate chains, summed at the end.
+              const int chain = T == 1 ? h : 0;
+              acc[u][chain] = E::mfma(w[2 * st + h], __builtin_bit_cast(vec_t, kk[u][st]), acc[u][chain]);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < T; ++u) {
+          const f32x4 v = T == 1 ? acc[u][0] + acc[u][1] : acc[u][0];
+          if constexpr (NCH == 1 || P == 0) {
+            best[u] = v;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) best[u][i] = max_prop(best[u][i], v[i]);
           }
         }
         if constexpr (NCH == 1 || P == 1) {
           retire();
-          pend0 = best0;
-          pend1 = best1;
+#pragma unroll
+          for (int u = 0; u < T; ++u) pend[u] = best[u];
           pend_g = g0 + it / NCH;
         }
       };
@@ -435,26 +446,31 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
       }
       if (it < n_items) item(std::integral_constant<int, 0>{}, it, wa);  // odd count: NCH == 1 only
       retire();
-      f32x4 out0, out1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        out0[i] = F16 ? mx0[i] * o_scale[i] + rest0[i] * r_scale[i] : mx0[i] + rest0[i];
-        out1[i] = F16 ? mx1[i] * o_scale[i] + rest1[i] * r_scale[i] : mx1[i] + rest1[i];
+      for (int u = 0; u < T; ++u) {
+        f32x4 out;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          out[i] = F16 ? mx[u][i] * o_scale[i] + rest[u][i] * r_scale[i] : mx[u][i] + rest[u][i];
+        emit(mt_first + kStreams * u, out);
       }
-      emit(mt0, out0);
-      emit(mt1, out1);
     };
 
-    load_tile(pages, t0, t1, wave + 2 * kStreams, kn[0]);
-    load_tile(pages, t0, t1, wave + 3 * kStreams, kn[1]);
-    if (wave < n_mt) score_pair(wave, ka[0], wave + kStreams, ka[1]);
-    if (more) {
-      const int nt0 = t0 + kScoreTile;
-      const int nt1 = min(n, nt0 + kScoreTile);
-      load_tile(next, nt0, nt1, wave, ka[0]);
-      load_tile(next, nt0, nt1, wave + kStreams, ka[1]);
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) {
+      const int cur = q & 1;
+      if (q + 1 < kGroups) {
+#pragma unroll
+        for (int u = 0; u < T; ++u) load_tile(pages, t0, t1, wave + kStreams * ((q + 1) * T + u), kbuf[cur ^ 1][u]);
+      } else if (more) {
+        const int nt0 = t0 + kScoreTile;
+        const int nt1 = min(n, nt0 + kScoreTile);
+#pragma unroll
+        for (int u = 0; u < T; ++u) load_tile(next, nt0, nt1, wave + kStreams * u, kbuf[cur ^ 1][u]);
+      }
+      const int mt_first = wave + kStreams * q * T;
+      if (mt_first < n_mt) score_group(mt_first, kbuf[cur]);
     }
-    if (wave + 2 * kStreams < n_mt) score_pair(wave + 2 * kStreams, kn[0], wave + 3 * kStreams, kn[1]);
 
     __syncthreads();
 
