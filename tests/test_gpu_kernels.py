@@ -346,6 +346,44 @@ def test_aggregate_single_layer_rsqrt_form(hip_device) -> None:
     torch.testing.assert_close(agg.cpu(), want2, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("layer_mode", ["mean", "max"])
+def test_aggregate_row_stride_invariance(hip_device, layer_mode) -> None:
+    # kvc_aggregate on head-major scores with ragged, unaligned sequence starts
+    # gives the same bits whatever the row stride, NaN and +-inf included.
+    from kvcompress_mi355x import _native
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    g = torch.Generator().manual_seed(21)
+    lens = [1, 3, 5, 1000, 4097, 2]
+    total = sum(lens)
+    layers, heads = 3, 7
+    offs = [0]
+    for n in lens:
+        offs.append(offs[-1] + n)
+    base = torch.randn(layers, heads, total, generator=g) * 2
+    base[1, 3, 7] = float("nan")
+    base[0, 0, 1500] = float("inf")
+    base[2, 5, 9] = float("-inf")
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=hip_device)
+    tok_off = torch.tensor(offs[:-1], dtype=torch.int64, device=hip_device)
+    mean = torch.randn(layers, len(lens), heads, generator=g).to(hip_device)
+    var = (torch.rand(layers, len(lens), heads, generator=g) + 0.1).to(hip_device)
+    mode = _native.LAYER_MEAN if layer_mode == "mean" else _native.LAYER_MAX
+    outs = []
+    for row in (total + (-total) % 4 + 64, total + 1 + ((total + 1) % 4 == 0)):
+        raw = torch.full((layers, heads, row), float("nan"), device=hip_device)
+        raw[:, :, :total] = base.to(hip_device)
+        agg = torch.full((total,), 123.0, device=hip_device)
+        _native.call(
+            "kvc_aggregate", dev.stream_handle(hip_device), layers, heads, len(lens), max(lens), dev.ptr(seq_lens),
+            dev.ptr(tok_off), dev.ptr(raw), heads * row, 1, row, dev.ptr(mean), dev.ptr(var), len(lens) * heads, heads,
+            mode, _native.AGG_FINALIZE, dev.ptr(agg),
+        )
+        outs.append(agg.cpu())
+    assert outs[0].view(torch.int32).equal(outs[1].view(torch.int32))
+    assert not torch.isnan(outs[0]).any() and bool((outs[0] != 123.0).all())
+
+
 # ----------------------------------------------------------------- select --
 
 
