@@ -172,9 +172,13 @@ def test_score_paged_matches_oracle(hip_device, case) -> None:
 MAX_CASES = [
     # (kv, qpk, head_dim, rotary, style, dtype, tokens, max_model_len -> offsets)
     (8, 5, 128, 128, "half", torch.bfloat16, 1000, 32768),        # 16 offsets, one chunk
-    (8, 5, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: two chunks, two head groups
+    (8, 5, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: a chunk per head + a shared tail chunk
+    (4, 8, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: two chunks per head, two head groups
+    (4, 5, 128, 128, "half", torch.bfloat16, 900, 65536),         # 17: tail rows of one offset, 16 heads a chunk
+    (2, 3, 128, 64, "half", torch.bfloat16, 800, 1 << 23),        # 24: two heads per tail chunk, two tail chunks
+    (2, 1, 128, 128, "half", torch.bfloat16, 400, 1 << 20),       # 21: one query head, partly filled tail chunk
     (2, 4, 128, 128, "half", torch.bfloat16, 5000, 32768),        # several spans per workgroup
-    (2, 8, 256, 64, "half", torch.bfloat16, 700, 262144),         # partial RoPE, 19 offsets
+    (2, 8, 256, 64, "half", torch.bfloat16, 700, 262144),         # partial RoPE, 19 offsets (two tail chunks)
     (8, 5, 128, 128, "half", torch.float16, 513, 32768),
     (8, 5, 128, 128, "interleaved", torch.bfloat16, 600, 131072),
     (2, 8, 256, 64, "interleaved", torch.float16, 300, 32768),

@@ -131,6 +131,47 @@ __global__ __launch_bounds__(256) void fold_offsets_kernel(OffsetFoldArgs m) {
   if (lane == 0) m.inv_scale[col] = F16 ? ldexpf(1.0f, -sh) : 1.0f;
 }
 
+// Tail chunks: one thread per (sequence, layer, KV head, tail chunk, step,
+// operand lane).  Row j of chunk tc is offset 16 + j % R of query head
+// tc * HT + j / R; rows past the chunk's heads repeat its first row (their
+// values are never part of a maximum).
+__global__ __launch_bounds__(256) void fold_offsets_tail_bf16_kernel(OffsetFoldArgs m, int tail_r, int tail_ht,
+                                                                     int tail_n, int64_t tail_base) {
+  typedef MfmaElem<false> E;
+  const FoldArgs& a = m.f;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t items = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * tail_n * m.nr * 64;
+  if (idx >= items) return;
+  const int lane = static_cast<int>(idx & 63);
+  const int st = static_cast<int>((idx >> 6) % m.nr);
+  int64_t r = (idx >> 6) / m.nr;
+  const int tc = static_cast<int>(r % tail_n);
+  r /= tail_n;
+  const int head = static_cast<int>(r % a.kv_heads);
+  r /= a.kv_heads;
+  const int layer = static_cast<int>(r % a.n_layers);
+  const int b = static_cast<int>(r / a.n_layers);
+  const int j = lane & 15, kb = lane >> 4;
+  int hl = j / tail_r, jj = j - (j / tail_r) * tail_r;
+  if (hl >= tail_ht || tc * tail_ht + hl >= a.qpk) hl = jj = 0;
+  const int g = tc * tail_ht + hl;
+  const int64_t row = (static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + g;
+  const int o = 16 + jj;
+  u32x4 hi, lo;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float v0 = offset_weight(a, b, layer, row, o, m.n_offsets, 32 * st + 8 * kb + 2 * w);
+    const float v1 = offset_weight(a, b, layer, row, o, m.n_offsets, 32 * st + 8 * kb + 2 * w + 1);
+    const uint32_t h = E::pack(v0, v1);
+    hi[w] = h;
+    lo[w] = E::pack(v0 - E::lo(h), v1 - E::hi(h));
+  }
+  const int64_t chunk = ((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * tail_n + tc;
+  u32x4* dst = m.frags + tail_base + (chunk * m.nr + st) * 128 + lane;
+  dst[0] = hi;
+  dst[64] = lo;
+}
+
 // Keys of pages the block table does not resolve read as zeros from here
 // (the furthest load reads 16 bytes at element 32 * (NK - 1) + 24).
 __device__ __attribute__((aligned(16))) uint32_t kZeroKeys[8 * 16];
@@ -179,8 +220,13 @@ __global__ __launch_bounds__(256) void fold_offsets_bf16_kernel(OffsetFoldArgs m
 struct MaxGeometry {
   int gpg;     // query heads per workgroup
   int groups;  // query-head groups per KV head
-  int nch;     // 16-offset chunks
+  int nch;     // 16-offset chunks per query head
   int work;    // (span set, KV head) items
+  // Shared tail chunks (16 < offsets <= 24, bf16): offsets 16.. of tail_ht
+  // query heads per chunk, tail_r rows each; tail_n chunks per KV head, at
+  // tail_base (16-byte words) in the fragment region.
+  int tail_r, tail_ht, tail_n;
+  int64_t tail_base;
 };
 
 template <int NK, int NF, int NCH, bool F16, bool IL>
@@ -226,6 +272,11 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     const int count = gcnt * kFragPerG;
 #pragma unroll 4
     for (int i = threadIdx.x; i < count; i += kScoreThreads) lds_frag[i] = src[i];
+    if (geo.tail_n > 0) {  // tail chunks after the heads' chunks (one group holds every head)
+      const int tcount = geo.tail_n * NR * 128;
+      const u32x4* tsrc = off_frags + geo.tail_base + (col0 / qpk) * tcount;
+      for (int i = threadIdx.x; i < tcount; i += kScoreThreads) lds_frag[count + i] = tsrc[i];
+    }
   }
 
   // Magnitude and pass fragments (packed [frag][kb][g < qpk], rotary weights
@@ -446,6 +497,44 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
       }
       if (it < n_items) item(std::integral_constant<int, 0>{}, it, wa);  // odd count: NCH == 1 only
       retire();
+      // Tail chunks: each head's maximum over its rows, folded into its lane's
+      // maximum over offsets 0..15.
+      for (int tc = 0; tc < geo.tail_n; ++tc) {
+        const u32x4* wl = lds_frag + (n_items + tc) * NR * 128 + lane;
+        f32x4 acc[T][2];
+#pragma unroll
+        for (int u = 0; u < T; ++u) acc[u][0] = acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < NR; ++st) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const vec_t w = __builtin_bit_cast(vec_t, wl[st * 128 + h * 64]);
+#pragma unroll
+            for (int u = 0; u < T; ++u) {
+              const int chain = T == 1 ? h : 0;
+              acc[u][chain] = E::mfma(w, __builtin_bit_cast(vec_t, kk[u][st]), acc[u][chain]);
+            }
+          }
+        }
+        for (int hl = 0; hl < geo.tail_ht; ++hl) {
+          const int g = tc * geo.tail_ht + hl;
+          if (g >= qpk) break;  // the same for every lane
+          const int lo_row = hl * geo.tail_r, hi_row = lo_row + geo.tail_r;
+#pragma unroll
+          for (int u = 0; u < T; ++u) {
+            const f32x4 v = T == 1 ? acc[u][0] + acc[u][1] : acc[u][0];
+            f32x4 mine;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int row = 4 * kb + i;
+              mine[i] = row >= lo_row && row < hi_row ? v[i] : -INFINITY;
+            }
+            const float tmax = token_max(mine);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx[u][i] = (4 * kb + i == g) ? max_prop(mx[u][i], tmax) : mx[u][i];
+          }
+        }
+      }
 #pragma unroll
       for (int u = 0; u < T; ++u) {
         f32x4 out;
@@ -704,7 +793,9 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   geo.nch = offset_chunks(n_offsets);
   if (geo.nch > 2)
     return fail(KVC_EINVAL, "kvc_score_paged_max: at most 32 offsets (got %d; 2^0 .. 2^30 are 31)", n_offsets);
-  const int nch = geo.nch;
+  int nch = geo.nch;
+  geo.tail_r = geo.tail_ht = geo.tail_n = 0;
+  geo.tail_base = 0;
   if (!mfma_scorer_supported(s, dtype, fa.interleaved ? KVC_ROPE_INTERLEAVED : KVC_ROPE_HALF)) {
     const size_t lds = sizeof(float) * (2 * static_cast<size_t>(16 * nch) * s.freq + s.freq + s.pass);
     if (lds > static_cast<size_t>(kValuMaxLds))
@@ -718,11 +809,27 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
     vk<<<grid, 256, lds, stream>>>(sa, fa, s.qpk, n_offsets);
     return launch_status("kvc_score_paged_max");
   }
+  // 17 to 24 offsets (bf16): each query head keeps one 16-offset chunk and the
+  // remaining 1-8 offsets of several heads share tail chunks, when every head
+  // of the KV head then fits one workgroup (18 offsets, 5 query heads, 128
+  // dims: 6 chunk passes per tile instead of 10, and keys read once).
+  const int64_t cols_total = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
+  if (!f16 && n_offsets > 16 && n_offsets <= 24) {
+    const int r = n_offsets - 16, ht = 16 / r, tn = (s.qpk + ht - 1) / ht;
+    if ((s.qpk + tn) * nr * 2 * kOffsetFragBytes <= kMaxFragLds) {
+      geo.nch = nch = 1;
+      geo.tail_r = r;
+      geo.tail_ht = ht;
+      geo.tail_n = tn;
+      geo.tail_base = cols_total * nr * 128;
+    }
+  }
   MaxKernel kern = f16 ? (fa.interleaved ? pick_max_typed<true, true>(nk, nf, nch) : pick_max_typed<true, false>(nk, nf, nch))
                        : (fa.interleaved ? pick_max_typed<false, true>(nk, nf, nch) : pick_max_typed<false, false>(nk, nf, nch));
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged_max: no scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
   const int per_g = geo.nch * nr * 2 * kOffsetFragBytes;
   int gpg = kMaxFragLds / per_g;
+  if (geo.tail_n > 0) gpg = s.qpk;
   if (gpg < 1)
     return fail(KVC_EINVAL, "kvc_score_paged_max: %d offsets need %d bytes of fragments per query head (limit %d)",
                 n_offsets, per_g, kMaxFragLds);
@@ -751,10 +858,16 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   else
     fold_offsets_bf16_kernel<<<static_cast<unsigned>(ceil_div(cols * geo.nch * nr * 64, 256)), 256, 0, stream>>>(m);
   if (int rc = launch_status("kvc_score_paged_max(fold)")) return rc;
+  if (geo.tail_n > 0) {
+    const int64_t threads = cols / s.qpk * geo.tail_n * nr * 64;
+    fold_offsets_tail_bf16_kernel<<<static_cast<unsigned>(ceil_div(threads, 256)), 256, 0, stream>>>(
+        m, geo.tail_r, geo.tail_ht, geo.tail_n, geo.tail_base);
+    if (int rc = launch_status("kvc_score_paged_max(tail fold)")) return rc;
+  }
 
   const float* rest_scale =
       reinterpret_cast<const float*>(static_cast<const char*>(workspace) + mfma_fragment_only_bytes(s));
-  const size_t lds = static_cast<size_t>(geo.gpg) * per_g;
+  const size_t lds = static_cast<size_t>(geo.gpg) * per_g + static_cast<size_t>(geo.tail_n) * nr * 2 * kOffsetFragBytes;
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(s.n_seq), static_cast<unsigned>(s.n_layers));
   kern<<<grid, kScoreThreads, lds, stream>>>(sa, geo, s.qpk, static_cast<const u32x4*>(workspace), rest_scale, m.frags,
                                              m.inv_scale);
