@@ -265,6 +265,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
   const int kb = lane >> 4;  // K block of the operands, row block of D
   const int64_t col0 = ((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * qpk;
   constexpr int kFragPerG = NCH * NR * 2 * 64;
+  // Shared tail chunks exist for head_dim >= 128 only: at 64 dims their code
+  // would cost the kernel its third wave per SIMD.
+  constexpr bool kTail = NCH == 1 && !F16 && NK >= 4;
 
   // Stage this group's per-offset fragments.
   {
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     const int count = gcnt * kFragPerG;
 #pragma unroll 4
     for (int i = threadIdx.x; i < count; i += kScoreThreads) lds_frag[i] = src[i];
-    if (geo.tail_n > 0) {  // tail chunks after the heads' chunks (one group holds every head)
+    if constexpr (kTail) if (geo.tail_n > 0) {  // tail chunks after the heads' chunks (one group holds every head)
       const int tcount = geo.tail_n * NR * 128;
       const u32x4* tsrc = off_frags + geo.tail_base + (col0 / qpk) * tcount;
       for (int i = threadIdx.x; i < tcount; i += kScoreThreads) lds_frag[count + i] = tsrc[i];
@@ -499,7 +502,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
       retire();
       // Tail chunks: each head's maximum over its rows, folded into its lane's
       // maximum over offsets 0..15.
-      for (int tc = 0; tc < geo.tail_n; ++tc) {
+      for (int tc = 0; tc < (kTail ? geo.tail_n : 0); ++tc) {
         const u32x4* wl = lds_frag + (n_items + tc) * NR * 128 + lane;
         f32x4 acc[T][2];
 #pragma unroll
@@ -814,7 +817,7 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   // of the KV head then fits one workgroup (18 offsets, 5 query heads, 128
   // dims: 6 chunk passes per tile instead of 10, and keys read once).
   const int64_t cols_total = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
-  if (!f16 && n_offsets > 16 && n_offsets <= 24) {
+  if (!f16 && nk >= 4 && n_offsets > 16 && n_offsets <= 24) {
     const int r = n_offsets - 16, ht = 16 / r, tn = (s.qpk + ht - 1) / ht;
     if ((s.qpk + tn) * nr * 2 * kOffsetFragBytes <= kMaxFragLds) {
       geo.nch = nch = 1;
