@@ -388,6 +388,54 @@ def test_aggregate_row_stride_invariance(hip_device, layer_mode) -> None:
     assert not torch.isnan(outs[0]).any() and bool((outs[0] != 123.0).all())
 
 
+@pytest.mark.parametrize("layer_mode", ["mean", "max"])
+def test_aggregate_finalize_non_finite_matches_oracle(hip_device, layer_mode) -> None:
+    # Normalise, head max, layer mean/max and nan_to_num(nan=-inf, posinf=1e30)
+    # (tri/method.py:423-467) against the oracle's torch program, per sequence of
+    # a ragged batch, with NaN and +-inf planted in the raw scores.
+    from kvcompress_mi355x import _native
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    g = torch.Generator().manual_seed(33)
+    lens = [700, 45, 1301]
+    total, layers, heads = sum(lens), 3, 6
+    offs = [0, lens[0], lens[0] + lens[1]]
+    raw = torch.randn(layers, heads, total, generator=g) * 2 + 0.5
+    raw[1, 3, 7] = float("nan")                    # NaN head score -> NaN layer -> -inf
+    raw[0, 0, 500] = float("inf")                  # +inf -> 1e30
+    raw[2, 5, 9] = float("-inf")                   # one head -inf: the others' maximum
+    raw[0, :, 20] = float("-inf")                  # every head -inf: -inf
+    raw[0, 2, 730] = float("inf")                  # +inf in layer 0 ...
+    raw[1, :, 730] = float("-inf")                 # ... -inf in layer 1: NaN (mean) / +inf (max)
+    raw[2, 4, 800] = float("nan")
+    mean = torch.randn(layers, len(lens), heads, generator=g)
+    var = torch.rand(layers, len(lens), heads, generator=g) + 0.1
+    cfg = ref.MethodConfig(budget=1, recent=0, prefix=0, segments=1, policy="global", layer_aggregation=layer_mode)
+    want = []
+    for b, n in enumerate(lens):
+        part = raw[:, :, offs[b] : offs[b] + n].reshape(layers, 2, 3, n)  # [kv, qpk, tokens] per layer
+        stats = [(var[l, b].view(2, 3), mean[l, b].view(2, 3)) for l in range(layers)]
+        want.append(ref.aggregate_layers(list(part), stats, cfg))
+    want = torch.cat(want)
+    assert int(torch.isneginf(want).sum()) >= 2 and int((want == 1e30).sum()) >= 1
+    d = hip_device
+    agg = torch.full((total,), 123.0, device=d)
+    raw_d, mean_d, var_d = raw.to(d), mean.to(d), var.to(d)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=d)
+    tok_off = torch.tensor(offs, dtype=torch.int64, device=d)
+    _native.call(
+        "kvc_aggregate", dev.stream_handle(d), layers, heads, len(lens), max(lens), dev.ptr(seq_lens), dev.ptr(tok_off),
+        dev.ptr(raw_d), heads * total, 1, total, dev.ptr(mean_d), dev.ptr(var_d), len(lens) * heads, heads,
+        _native.LAYER_MEAN if layer_mode == "mean" else _native.LAYER_MAX, _native.AGG_FINALIZE, dev.ptr(agg),
+    )
+    got = agg.cpu()
+    finite = torch.isfinite(want) & (want != 1e30)
+    assert torch.equal(torch.isneginf(got), torch.isneginf(want)), "-inf positions differ"
+    assert torch.equal(got[want == 1e30], want[want == 1e30]), "+inf must finalise to 1e30"
+    assert not torch.isnan(got).any()
+    torch.testing.assert_close(got[finite], want[finite], rtol=1e-3, atol=1e-3)
+
+
 # ----------------------------------------------------------------- select --
 
 
