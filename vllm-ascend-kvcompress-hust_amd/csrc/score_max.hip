@@ -842,6 +842,9 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   const int64_t items = ceil_div(s.max_tiles, kMaxSpans) * s.kv_heads;
   const int64_t gx = ceil_div(items, 8) * 8 * geo.groups;
   if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_score_paged_max: grid too large");
+  if (cols_total * geo.nch * nr * 64 > 0x7fffffff)  // threads of the weight fold
+    return fail(KVC_EINVAL, "kvc_score_paged_max: %lld weight columns exceed one fold launch",
+                static_cast<long long>(cols_total));
   geo.work = static_cast<int>(items);
 
   FoldArgs rest = fa;
