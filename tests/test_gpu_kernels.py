@@ -177,6 +177,8 @@ MAX_CASES = [
     (4, 5, 128, 128, "half", torch.bfloat16, 900, 65536),         # 17: tail rows of one offset, 16 heads a chunk
     (2, 3, 128, 64, "half", torch.bfloat16, 800, 1 << 23),        # 24: two heads per tail chunk, two tail chunks
     (2, 1, 128, 128, "half", torch.bfloat16, 400, 1 << 20),       # 21: one query head, partly filled tail chunk
+    (2, 5, 128, 64, "interleaved", torch.bfloat16, 500, 1 << 23),  # 24: three tail chunks, partial RoPE
+    (2, 8, 128, 64, "half", torch.bfloat16, 300, 1 << 23),        # 24: four tail chunks, LDS exactly full
     (2, 4, 128, 128, "half", torch.bfloat16, 5000, 32768),        # several spans per workgroup
     (2, 8, 256, 64, "half", torch.bfloat16, 700, 262144),         # partial RoPE, 19 offsets (two tail chunks)
     (8, 5, 128, 128, "half", torch.float16, 513, 32768),
