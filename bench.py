@@ -82,155 +82,12 @@ def parse_args() -> argparse.Namespace:
         "work on the default workload)",
     )
     p.add_argument(
-        "--calibrate-copy-mib",
-        type=int,
-        default=0,
-        help="only run a plain device copy of this many MiB (3 times) to scale HBM byte counters",
-    )
-    p.add_argument(
-        "--probe-bandwidth",
-        action="store_true",
-        help="only measure streaming read / write / copy ceilings of this GPU (4 GiB buffers)",
-    )
-    p.add_argument(
         "--calibration",
         action="store_true",
         help="only measure calibration statistics (kvc_qstats_accumulate) over a Qwen2.5-14B-shaped calibration "
         "pass: 48 layers of 4096-token bf16 query projections (40 heads x 128), one buffer per layer",
     )
-    p.add_argument(
-        "--placement-sweep",
-        type=int,
-        default=0,
-        help="only re-allocate the workload's KV pool as one arena this many times (freeing it in between) "
-        "and report compaction time and streaming rates inside each allocation",
-    )
     return p.parse_args()
-
-
-def probe_bandwidth() -> int:
-    """Achievable HBM ceilings: kvc_bandwidth_probe read / write / copy of
-    4 GiB in 16-byte words, with and without non-temporal hints, over a range
-    of grid sizes, and the block-contiguous pipelined copy; reports the best
-    rate of each kind in GB/s."""
-    import torch
-
-    from kvcompress_mi355x import _native
-
-    lib = _native.load()
-    size = 4 << 30
-    src = torch.empty(size, dtype=torch.uint8, device="cuda:0")
-    src.random_()
-    dst = torch.empty_like(src)
-    stream = torch.cuda.current_stream().cuda_stream
-    best: dict[str, float] = {}
-    detail: dict[str, float] = {}
-    for kind, name, passes in ((0, "read", 1), (1, "write", 1), (2, "copy", 2), (3, "copy_chunked", 2)):
-        for nt in ((0, 1) if kind < 3 else (1,)):
-            for blocks in ((2048, 8192, 32768) if kind < 3 else (4096, 16384)):
-                for _ in range(2):
-                    _native.check(lib.kvc_bandwidth_probe(stream, kind, nt, src.data_ptr(), dst.data_ptr(), size, blocks), "probe")
-                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                start.record()
-                for _ in range(5):
-                    lib.kvc_bandwidth_probe(stream, kind, nt, src.data_ptr(), dst.data_ptr(), size, blocks)
-                end.record()
-                torch.cuda.synchronize()
-                gbs = passes * size / (start.elapsed_time(end) / 5) / 1e6
-                detail[f"{name}_nt{nt}_blocks{blocks}"] = round(gbs, 1)
-                best[name] = max(best.get(name, 0.0), round(gbs, 1))
-    print(json.dumps({"hbm_ceiling_gbs": best, "peak_gbs": HBM_PEAK_GBS, "detail": detail}), flush=True)
-    return 0
-
-
-def _stream_rates(lib, buf) -> dict[str, float]:
-    """Streaming read / write / block-contiguous copy (non-temporal, 8 GiB or
-    less) between the first and the second half of a device buffer, in GB/s."""
-    import torch
-
-    from kvcompress_mi355x import _native
-
-    raw = buf.view(-1).view(torch.uint8)
-    half = (raw.numel() // 2) // (1 << 30) * (1 << 30)
-    size = min(8 << 30, half)
-    if size <= 0:
-        raise ValueError("buffer too small for the streaming probe")
-    src, dst = raw[:size], raw[half : half + size]
-    stream = torch.cuda.current_stream().cuda_stream
-    rates = {}
-    for kind, name, passes, blocks in ((0, "read", 1, 32768), (1, "write", 1, 32768), (3, "copy", 2, 16384)):
-        _native.check(lib.kvc_bandwidth_probe(stream, kind, 1, src.data_ptr(), dst.data_ptr(), size, blocks), "probe")
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(3):
-            lib.kvc_bandwidth_probe(stream, kind, 1, src.data_ptr(), dst.data_ptr(), size, blocks)
-        end.record()
-        torch.cuda.synchronize()
-        rates[name] = round(passes * size / (start.elapsed_time(end) / 3) / 1e6, 1)
-    return rates
-
-
-def placement_sweep(config: int, times: int) -> int:
-    """The same KV pool placed `times` times in fresh device memory: each pass
-    allocates one arena, copies the workload's K/V pages into it, times
-    kvc_compact on it and the streaming rates inside it, and frees it."""
-    import dataclasses
-    import gc
-
-    import torch
-
-    from kvcompress_mi355x import _native, workloads
-
-    lib = _native.load()
-    spec = workloads.config_spec(config)
-    device = torch.device("cuda:0")
-    ref = workloads.build_synthetic_cache(spec, device, seed=0)
-    shape = tuple(ref.k_caches[0].shape)
-    n_pages = shape[0]
-    for i in range(times):
-        pool = torch.empty((2 * spec.n_layers * n_pages,) + shape[1:], dtype=spec.dtype, device=device)
-        ks, vs = [], []
-        for layer in range(spec.n_layers):
-            k = pool[(2 * layer) * n_pages : (2 * layer + 1) * n_pages]
-            v = pool[(2 * layer + 1) * n_pages : (2 * layer + 2) * n_pages]
-            k.copy_(ref.k_caches[layer])
-            v.copy_(ref.v_caches[layer])
-            ks.append(k)
-            vs.append(v)
-        cache = dataclasses.replace(ref, k_caches=ks, v_caches=vs)
-        pipeline, batch = workloads.build_pipeline(cache)
-        pipeline.step(batch)
-        for _ in range(3):
-            pipeline.compact(batch)
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(10):
-            pipeline.compact(batch)
-        end.record()
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / 10
-        line = {"placement": i, "arena_gib": round(pool.numel() * 2 / 2**30, 1), "compact_ms": round(ms, 4)}
-        line.update({f"{k}_gbs": v for k, v in _stream_rates(lib, pool).items()})
-        print(json.dumps(line), flush=True)
-        del pool, ks, vs, cache, pipeline, batch
-        gc.collect()
-        torch.cuda.empty_cache()
-    return 0
-
-
-def calibrate_copy(mib: int) -> int:
-    """A plain float32 device copy of known size, for scaling the profiler's
-    FETCH_SIZE / WRITE_SIZE counters to bytes."""
-    import torch
-
-    n = mib * (1 << 20) // 4
-    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 3}), flush=True)
-    return 0
 
 
 def calibration_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -> int:
@@ -440,6 +297,7 @@ def cpu_baseline(cache, spec, repeats: int, score_aggregation: str = "mean") -> 
     sequence: score the sampled layers, select, materialise every layer."""
     import torch
 
+    from oracle import stats_ref
     from oracle import triattention_ref as ref
 
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -454,11 +312,17 @@ def cpu_baseline(cache, spec, repeats: int, score_aggregation: str = "mean") -> 
     h_dst = torch.tensor([remap[int(p)] for p in dst.tolist()])
     k_host = [k[pages].cpu() for k in cache.k_caches]
     v_host = [v[pages].cpu() for v in cache.v_caches]
-    stats = cache.calibration.to_device(spec.model_shape(), torch.device("cpu"))
-    layer_stats = [
-        ref.LayerStats(s.q_mean_real, s.q_mean_imag, s.q_abs_mean, s.freq_scale_sq, s.omega, s.rope_style, s.rotary_dim, s.q_pass_mean)
-        for s in (stats[layer] for layer in spec.scoring_layers)
-    ]
+    model = spec.model_shape()
+    laid_out = stats_ref.layer_stats_for_device(
+        cache.calibration.layers,
+        cache.calibration.metadata,
+        num_attention_heads=model.num_attention_heads,
+        num_kv_heads=model.num_kv_heads,
+        head_dim=model.head_dim,
+        rotary_dim=model.effective_rotary_dim,
+        rope_theta=model.rope_theta,
+    )
+    layer_stats = [laid_out[layer] for layer in spec.scoring_layers]
     cfg = ref.MethodConfig(
         budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
         score_aggregation=score_aggregation, score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
@@ -500,12 +364,6 @@ def main() -> int:
 
     from kvcompress_mi355x import workloads
 
-    if args.calibrate_copy_mib:
-        return calibrate_copy(args.calibrate_copy_mib)
-    if args.probe_bandwidth:
-        return probe_bandwidth()
-    if args.placement_sweep:
-        return placement_sweep(args.config, args.placement_sweep)
     if args.calibration:
         return calibration_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
     if not torch.cuda.is_available():

@@ -356,19 +356,6 @@ int kvc_qstats_accumulate(kvc_stream_t stream, int dtype, const void* q, int64_t
 int kvc_qstats_finish(kvc_stream_t stream, int heads, int head_dim, int rotary_dim, const void* state,
                       double* real_sum, double* imag_sum, double* abs_sum, double* pass_sum);
 
-/* ------------------------------------------------------- measurement -- */
-
-/* Streaming HBM probe (no counterpart in the reference; used to state the
- * achievable ceilings beside the roofline): kind 0 = read `bytes` from src
- * (dst receives at most one word), 1 = write `bytes` to dst, 2 = copy src ->
- * dst; 16-byte words, grid-stride over `blocks` workgroups of 256 threads,
- * optionally with non-temporal hints.  Kind 3 = copy in `blocks` contiguous
- * chunks of 512-thread workgroups, the next 8 words per thread loaded before
- * the current ones are stored, non-temporal (`nontemporal` ignored).  bytes
- * must be a multiple of 16. */
-int kvc_bandwidth_probe(kvc_stream_t stream, int kind, int nontemporal, const void* src, void* dst,
-                        int64_t bytes, int blocks);
-
 #ifdef __cplusplus
 }
 #endif

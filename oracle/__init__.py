@@ -21,8 +21,16 @@ Parity pins (how each oracle function is checked, see tests/test_oracle_*.py):
   score_post_rope_keys      reference KATs (tests/test_scoring.py:53-133: slow
                             per-offset reference, scale 4.0, partial-RoPE
                             [2,-5]); float64 brute force; omega=0 closed form
-  normalize/aggregate       closed form of tests/test_selection.py:271-280;
-                            float64 brute force
+  normalize_head_scores     single-layer closed forms (population variance,
+                            1e-6 clamp, head maximum); float64 brute force
+  aggregate_layers          tests/test_oracle_aggregate.py: the two-layer
+                            closed form of tests/test_selection.py:230-280
+                            (mean and max, no collective) from exact power
+                            sums; six layers (division by the scoring-layer
+                            count); layer 0 counted once; maximum over every
+                            KV and query head; nan_to_num mapping after the
+                            layer combination (tri/method.py:463-467), NaN-
+                            propagating maximum, +inf -> 1e30, -inf kept
   select_keep_indices       reference KATs ([0,1,4,5], v3 evicts {2,5,8,11},
                             uneven quota count); brute-force sort; batched-v3
                             equivalence (tests/test_selection.py:94-125)

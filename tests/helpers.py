@@ -4,7 +4,24 @@ from __future__ import annotations
 
 import torch
 
+from oracle import stats_ref
 from oracle import triattention_ref as ref
+
+
+def oracle_layer_stats(calibration, model, layers) -> list[ref.LayerStats]:
+    """The oracle's statistics of ``layers`` from a loaded calibration, laid out
+    by the oracle's restatement of the device layout (oracle.stats_ref), not by
+    the product's CalibrationStats.to_device."""
+    laid_out = stats_ref.layer_stats_for_device(
+        calibration.layers,
+        calibration.metadata,
+        num_attention_heads=model.num_attention_heads,
+        num_kv_heads=model.num_kv_heads,
+        head_dim=model.head_dim,
+        rotary_dim=model.effective_rotary_dim,
+        rope_theta=model.rope_theta,
+    )
+    return [laid_out[layer] for layer in layers]
 
 
 def oracle_stats(device_stats) -> ref.LayerStats:

@@ -25,7 +25,7 @@ import gc
 import pytest
 import torch
 
-from helpers import assert_agg_close, assert_keep_matches, assert_scores_close, oracle_stats
+from helpers import assert_agg_close, assert_keep_matches, assert_scores_close, oracle_layer_stats
 from oracle import triattention_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -135,7 +135,6 @@ def _host_keys(cache, spec, b: int):
 def _oracle_sequence(cache, spec, pipeline, batch, b: int, host_keys) -> int:
     """Oracle on sequence b over its host key copies."""
     k_host, h_src = host_keys
-    stats = cache.calibration.to_device(spec.model_shape(), torch.device("cpu"))
     cfg = ref.MethodConfig(
         budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
         score_aggregation=pipeline.score_aggregation, score_chunk_size=8192, score_layer_stride=spec.score_layer_stride,
@@ -143,7 +142,7 @@ def _oracle_sequence(cache, spec, pipeline, batch, b: int, host_keys) -> int:
     n = spec.seq_lens[b]
     out = ref.method_select(
         k_host,
-        [oracle_stats(stats[layer]) for layer in spec.scoring_layers],
+        oracle_layer_stats(cache.calibration, spec.model_shape(), spec.scoring_layers),
         h_src,
         n,
         cache.round_starts[b],

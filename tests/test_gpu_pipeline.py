@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_agg_close, assert_keep_matches, assert_scores_close, oracle_stats
+from helpers import assert_agg_close, assert_keep_matches, assert_scores_close, oracle_layer_stats
 from oracle import triattention_ref as ref
 
 pytestmark = pytest.mark.gpu
@@ -19,8 +19,7 @@ GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
 def _oracle_for(host, spec, b, score_aggregation="mean", layer_aggregation="mean"):
-    stats = host.calibration.to_device(spec.model_shape(), torch.device("cpu"))
-    layer_stats = [oracle_stats(stats[layer]) for layer in spec.scoring_layers]
+    layer_stats = oracle_layer_stats(host.calibration, spec.model_shape(), spec.scoring_layers)
     cfg = ref.MethodConfig(
         budget=spec.budget, recent=spec.recent, prefix=spec.prefix, segments=spec.segments, policy=spec.policy,
         score_aggregation=score_aggregation, layer_aggregation=layer_aggregation,

@@ -11,7 +11,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-from helpers import assert_keep_matches, oracle_stats
+from helpers import assert_keep_matches, oracle_layer_stats
 from oracle import brute
 from oracle import triattention_ref as ref
 
@@ -106,7 +106,7 @@ def test_transaction_round_trip(hip_device, tmp_path) -> None:
     for b, r in enumerate(sorted(prompts)):
         out = ref.method_select(
             [host.k_caches[layer] for layer in spec.scoring_layers],
-            [oracle_stats(s) for s in (host.calibration.to_device(spec.model_shape(), torch.device("cpu"))[l] for l in spec.scoring_layers)],
+            oracle_layer_stats(host.calibration, spec.model_shape(), spec.scoring_layers),
             host.source_tables[b],
             spec.seq_lens[b],
             host.round_starts[b],

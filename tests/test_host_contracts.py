@@ -325,6 +325,30 @@ def test_max_scorer_queries_and_validation_without_gpu() -> None:
     assert "workspace too small" in lib.kvc_last_error().decode()
 
 
+def test_max_scorer_rejects_oversized_fold_before_launch() -> None:
+    """A bf16 shape whose per-offset weight fold would need more work-items than
+    one dispatch holds (4096 sequences x 64 layers x 8 KV heads x 5 query heads,
+    32 offsets: 5.4e9 fold threads) is rejected with KVC_EINVAL by the host
+    check, which runs before any launch."""
+    import torch
+
+    from kvcompress_mi355x import _native
+
+    if torch.cuda.is_available():
+        pytest.skip("placeholder pointers: run where no device could be reached by a launch")
+    lib = _native.load()
+    n_layers, kv, head_dim, qpk, n_seq, max_len, n_off = 64, 8, 128, 5, 4096, 256, 32
+    ws = lib.kvc_score_max_workspace_bytes(n_layers, kv, head_dim, head_dim, qpk, n_seq, max_len, n_off)
+    assert ws > 0
+    fake = 4096
+    rc = lib.kvc_score_paged_max(
+        None, 0, n_layers, fake, 100, 128 * kv * head_dim, kv, head_dim, head_dim, qpk, 0, n_seq, max_len, fake,
+        fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, n_off, 0, fake, 0, 1, 256, fake, ws,
+    )
+    assert rc == _native.EINVAL
+    assert "exceed one dispatch" in lib.kvc_last_error().decode()
+
+
 def test_raw_layout_names_the_scorer_without_gpu() -> None:
     """Matrix-core shapes (bf16 or fp16, half or interleaved RoPE, head_dim and
     F multiples of 32, qpk <= 8) get head-major raw scores; the rest token-major."""
@@ -345,3 +369,11 @@ def test_raw_layout_names_the_scorer_without_gpu() -> None:
     for args, want in cases:
         assert lib.kvc_score_raw_layout(*args) == want, args
     assert lib.kvc_score_raw_layout(7, half, 8, 128, 128, 5) < 0  # unknown dtype
+
+
+def test_backward_compatible_config_alias():
+    # tri/method.py:518-519, exported at tri/__init__.py:7,15.
+    from kvcompress_mi355x.methods import triattention
+
+    assert triattention.TriAttentionAscendConfig is TriAttentionConfig
+    assert "TriAttentionAscendConfig" in triattention.__all__

@@ -180,4 +180,11 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
 // into `weights`, laid out as the MFMA scorer reads them.
 int launch_mfma_fold(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, void* weights);
 
+// A dispatch's grid size in work-items is a 32-bit field of the dispatch
+// packet; every launch of the scorers checks its own grid against it before
+// the first launch of an entry point.
+constexpr int64_t kMaxDispatchItems = 0xffffffffLL;
+// Work-items of launch_mfma_fold's dispatch for this shape and dtype.
+int64_t mfma_fold_items(const ScoreShape& s, int dtype);
+
 }  // namespace kvc

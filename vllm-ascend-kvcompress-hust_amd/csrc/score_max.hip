@@ -842,8 +842,16 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   const int64_t items = ceil_div(s.max_tiles, kMaxSpans) * s.kv_heads;
   const int64_t gx = ceil_div(items, 8) * 8 * geo.groups;
   if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_score_paged_max: grid too large");
-  if (cols_total * geo.nch * nr * 64 > 0x7fffffff)  // threads of the weight fold
-    return fail(KVC_EINVAL, "kvc_score_paged_max: %lld weight columns exceed one fold launch",
+  // Every fold this call launches, checked before the first of them: the
+  // magnitude/pass fold, the per-offset fold (fp16: one wave per column, four
+  // per workgroup; bf16: one thread per fragment lane) and the tail fold.
+  const int64_t offset_items =
+      f16 ? ceil_div(cols_total, 4) * 256 : ceil_div(cols_total * geo.nch * nr * 64, 256) * 256;
+  const int64_t tail_items =
+      geo.tail_n > 0 ? ceil_div(cols_total / s.qpk * geo.tail_n * nr * 64, 256) * 256 : 0;
+  const int64_t fold_items = std::max(mfma_fold_items(s, dtype), std::max(offset_items, tail_items));
+  if (fold_items > kMaxDispatchItems)
+    return fail(KVC_EINVAL, "kvc_score_paged_max: the weight folds of %lld columns exceed one dispatch",
                 static_cast<long long>(cols_total));
   geo.work = static_cast<int>(items);
 
@@ -858,15 +866,13 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   m.nr = nr;
   m.frags = reinterpret_cast<u32x4*>(tail);
   m.inv_scale = reinterpret_cast<float*>(tail + (offset_fragment_bytes(s, n_offsets) + 255) / 256 * 256);
-  const int64_t cols = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
   if (f16)
-    fold_offsets_kernel<true><<<static_cast<unsigned>(ceil_div(cols, 4)), 256, 0, stream>>>(m);
+    fold_offsets_kernel<true><<<static_cast<unsigned>(offset_items / 256), 256, 0, stream>>>(m);
   else
-    fold_offsets_bf16_kernel<<<static_cast<unsigned>(ceil_div(cols * geo.nch * nr * 64, 256)), 256, 0, stream>>>(m);
+    fold_offsets_bf16_kernel<<<static_cast<unsigned>(offset_items / 256), 256, 0, stream>>>(m);
   if (int rc = launch_status("kvc_score_paged_max(fold)")) return rc;
   if (geo.tail_n > 0) {
-    const int64_t threads = cols / s.qpk * geo.tail_n * nr * 64;
-    fold_offsets_tail_bf16_kernel<<<static_cast<unsigned>(ceil_div(threads, 256)), 256, 0, stream>>>(
+    fold_offsets_tail_bf16_kernel<<<static_cast<unsigned>(tail_items / 256), 256, 0, stream>>>(
         m, geo.tail_r, geo.tail_ht, geo.tail_n, geo.tail_base);
     if (int rc = launch_status("kvc_score_paged_max(tail fold)")) return rc;
   }

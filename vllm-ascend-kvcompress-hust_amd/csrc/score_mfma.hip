@@ -442,16 +442,28 @@ bool mfma_scorer_supported(const ScoreShape& s, int dtype, int rope_style) {
   return pick(s.head_dim / 32, s.freq / 32, dtype, rope_style) != nullptr;
 }
 
+int64_t mfma_fold_items(const ScoreShape& s, int dtype) {
+  const MfmaGeometry geo = geometry(s);
+  const int64_t cols = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
+  // fp16: one wave per weight column, four per workgroup; bf16: one thread per
+  // live lane of every fragment.
+  if (dtype == KVC_DTYPE_FP16) return ceil_div(cols, 4) * 256;
+  return ceil_div(cols * (2 * geo.nk + 2 * geo.nf) * 4, 256) * 256;
+}
+
 int launch_mfma_fold(hipStream_t stream, const ScoreShape& s, int dtype, const FoldArgs& fa, void* weights) {
   const MfmaGeometry geo = geometry(s);
+  const int64_t items = mfma_fold_items(s, dtype);
+  if (items > kMaxDispatchItems)
+    return fail(KVC_EINVAL, "kvc_score_paged: the weight fold's %lld work-items exceed one dispatch",
+                static_cast<long long>(items));
   uint16_t* frags = static_cast<uint16_t*>(weights);
   float* inv_scale = reinterpret_cast<float*>(static_cast<char*>(weights) + mfma_fragment_only_bytes(s));
+  const unsigned blocks = static_cast<unsigned>(items / 256);
   if (dtype == KVC_DTYPE_FP16) {
-    const int64_t cols = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
-    fold_mfma_f16_kernel<<<static_cast<unsigned>(ceil_div(cols, 4)), 256, 0, stream>>>(fa, geo.nk, geo.nf, frags, inv_scale);
+    fold_mfma_f16_kernel<<<blocks, 256, 0, stream>>>(fa, geo.nk, geo.nf, frags, inv_scale);
   } else {
-    const int64_t fold_threads = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * (2 * geo.nk + 2 * geo.nf) * 4 * s.qpk;
-    fold_mfma_kernel<<<static_cast<unsigned>(ceil_div(fold_threads, 256)), 256, 0, stream>>>(fa, geo.nk, geo.nf, frags);
+    fold_mfma_kernel<<<blocks, 256, 0, stream>>>(fa, geo.nk, geo.nf, frags);
   }
   return launch_status("kvc_score_paged(fold)");
 }

@@ -88,7 +88,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_qstats_state_bytes": (_sz, [_i32, _i32, _i32]),
     "kvc_qstats_accumulate": (_i32, [_p, _i32, _p, _i64, _i64, _i32, _i32, _i32, _p, _sz]),
     "kvc_qstats_finish": (_i32, [_p, _i32, _i32, _i32, _p, _p, _p, _p, _p]),
-    "kvc_bandwidth_probe": (_i32, [_p, _i32, _i32, _p, _p, _i64, _i32]),
 }
 
 _LOCK = threading.Lock()

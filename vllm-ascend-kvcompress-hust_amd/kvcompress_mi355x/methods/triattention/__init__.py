@@ -3,6 +3,7 @@
 from .config import TriAttentionConfig
 from .method import (
     METHOD_NAME,
+    TriAttentionAscendConfig,
     TriAttentionLayerCache,
     TriAttentionMethod,
     create_triattention_method,
@@ -10,6 +11,7 @@ from .method import (
 
 __all__ = [
     "METHOD_NAME",
+    "TriAttentionAscendConfig",
     "TriAttentionConfig",
     "TriAttentionLayerCache",
     "TriAttentionMethod",

@@ -238,3 +238,8 @@ def create_triattention_method(
     options: Mapping[str, JsonScalar], vllm_config: Any, model_shape: ModelShape
 ) -> KVCompressionMethod:
     return TriAttentionMethod(options, vllm_config, model_shape)
+
+
+# Import name of the options type before the method registry existed
+# (tri/method.py:518-519); callers that still import it get the same class.
+TriAttentionAscendConfig = TriAttentionConfig
