@@ -176,6 +176,30 @@ int kvc_head_stats(kvc_stream_t stream, int n_layers, int kv_heads, int head_dim
                    int qpk, int n_seq, int max_seq_len, const int32_t* seq_lens,
                    const void* workspace, size_t workspace_bytes, float* mean, float* var);
 
+/* kvc_score_paged followed by kvc_head_stats, with the scorer's scratch (folded
+ * weights and per-tile partial sums) in a static 64 MiB device array that the
+ * library holds on every device it runs on until the process ends, instead of
+ * a caller workspace.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid allocation).  It allocates and frees nothing.  Arguments as
+ * kvc_score_paged without the workspace, plus kvc_head_stats's mean/var
+ * outputs; the results equal those two calls'.  Returns KVC_EINVAL when the
+ * batch needs more scratch than 64 MiB (kvc_score_workspace_bytes of the same
+ * shape; e.g. 6 scoring layers x 16 sequences of 16384 tokens x 40 query heads
+ * need 7 MiB) and when `stream` does not belong to the current device.  Every
+ * call on a device shares that device's array: calls that overlap in time on
+ * one device (concurrent streams, several threads) race and must be
+ * serialised by the caller. */
+int kvc_score_paged_noalloc(kvc_stream_t stream, int dtype, int n_layers, const uint64_t* k_layer_ptrs,
+                            int64_t num_pages, int64_t page_stride, int kv_heads, int head_dim,
+                            int rotary_dim, int qpk, int rope_style, int n_seq, int max_seq_len,
+                            const int32_t* seq_lens, const int64_t* token_offsets,
+                            const int64_t* block_offsets, const int64_t* block_ids, const float* q_real,
+                            const float* q_imag, const float* freq_scale, const float* extra_coef,
+                            const float* q_pass, const float* phase_cos, const float* phase_sin,
+                            int64_t phase_seq_stride, float* raw, int64_t raw_layer_stride,
+                            int64_t raw_token_stride, int64_t raw_head_stride, float* mean, float* var);
+
 /* Normalise, take the max over query heads and combine across layers
  * (normalize_head_scores + _aggregate_torch, tri/scoring.py:123-128,
  * tri/method.py:477-503; device form tri/kernels.py:365-437; layer mean and

@@ -19,7 +19,7 @@ REPO = PACKAGE_ROOT.parent
 INCLUDE = REPO / "include"
 OUTPUT = PACKAGE_ROOT / "kvcompress_mi355x" / "libkvcompress_mi355x.so"
 BUILD_DIR = CSRC / "_build"
-SOURCES = ("capi.hip", "score.hip", "score_mfma.hip", "score_max.hip", "select.hip", "compact.hip", "decode.hip", "calib.hip")
+SOURCES = ("capi.hip", "score.hip", "score_mfma.hip", "score_max.hip", "select.hip", "compact.hip", "decode.hip", "calib.hip", "noalloc.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

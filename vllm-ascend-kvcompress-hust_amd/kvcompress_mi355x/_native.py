@@ -62,6 +62,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ],
     ),
     "kvc_head_stats": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _sz, _p, _p]),
+    "kvc_score_paged_noalloc": (
+        _i32,
+        [
+            _p, _i32, _i32, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+            _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _i64, _p, _p,
+        ],
+    ),
     "kvc_aggregate": (
         _i32,
         [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _i32, _u32, _p],
