@@ -109,12 +109,12 @@ def test_model_shape_rejects(overrides, message) -> None:
 
 
 def test_builtin_text_and_explicit_input(tmp_path: Path) -> None:
-    text, source = calibration._load_calibration_text(CalibrationRequest(model="m", output=tmp_path / "s.pt", max_length=200))
+    text, source = calibration.calibration_text(CalibrationRequest(model="m", output=tmp_path / "s.pt", max_length=200))
     assert source == calibration.BUILTIN_INPUT_SOURCE
     assert len(text) >= 200 * 6
     path = tmp_path / "input.txt"
     path.write_text("hello calibration", encoding="utf-8")
-    text, source = calibration._load_calibration_text(CalibrationRequest(model="m", output=tmp_path / "s.pt", input_path=path))
+    text, source = calibration.calibration_text(CalibrationRequest(model="m", output=tmp_path / "s.pt", input_path=path))
     assert text == "hello calibration" and source == str(path.resolve())
 
 
@@ -122,9 +122,9 @@ def test_generator_rejects_empty_or_missing_input(tmp_path: Path) -> None:
     empty = tmp_path / "empty.txt"
     empty.write_text("  \n", encoding="utf-8")
     with pytest.raises(ValueError, match="empty"):
-        calibration._load_calibration_text(CalibrationRequest(model="m", output=tmp_path / "s.pt", input_path=empty))
+        calibration.calibration_text(CalibrationRequest(model="m", output=tmp_path / "s.pt", input_path=empty))
     with pytest.raises(ValueError, match="does not exist"):
-        calibration._load_calibration_text(
+        calibration.calibration_text(
             CalibrationRequest(model="m", output=tmp_path / "s.pt", input_path=tmp_path / "missing.txt")
         )
 
@@ -135,36 +135,36 @@ def test_generator_rejects_short_max_length(tmp_path: Path) -> None:
 
 
 def test_dtype_names() -> None:
-    assert calibration._dtype_name(torch.float16) == "float16"
-    assert calibration._dtype_name("half") == "float16"
-    assert calibration._dtype_name("auto") == "bfloat16"
-    assert calibration._torch_dtype("float") == torch.float32
+    assert calibration.dtype_name(torch.float16) == "float16"
+    assert calibration.dtype_name("half") == "float16"
+    assert calibration.dtype_name("auto") == "bfloat16"
+    assert calibration.torch_dtype("float") == torch.float32
     with pytest.raises(ValueError, match="unsupported"):
-        calibration._torch_dtype("int8")
+        calibration.torch_dtype("int8")
 
 
 def test_distributed_calibration_reports_missing_accelerate(tmp_path: Path, monkeypatch) -> None:
     request = CalibrationRequest(model="fake/model", output=tmp_path / "stats.pt", device_map="auto")
     monkeypatch.setattr(calibration.importlib.util, "find_spec", lambda name: None)
-    with pytest.raises(RuntimeError, match=r"\[calibration\]"):
-        calibration._generate_payload(request)
+    with pytest.raises(RuntimeError, match="accelerate"):
+        calibration._artifact(request)
 
 
 # ------------------------------------------------------------ fingerprints --
 
 
 def test_model_source_fingerprint(tmp_path: Path) -> None:
-    a = calibration._model_source_fingerprint("org/model", None)
+    a = calibration.model_source_fingerprint("org/model", None)
     assert a.startswith("identifier:")
-    assert a == calibration._model_source_fingerprint("org/model", "default")
-    assert a != calibration._model_source_fingerprint("org/model", "v2")
-    with pytest.raises(ValueError, match="no recognized checkpoint"):
-        calibration._model_source_fingerprint(str(tmp_path), None)
+    assert a == calibration.model_source_fingerprint("org/model", "default")
+    assert a != calibration.model_source_fingerprint("org/model", "v2")
+    with pytest.raises(ValueError, match="no checkpoint files"):
+        calibration.model_source_fingerprint(str(tmp_path), None)
     (tmp_path / "config.json").write_text("{}", encoding="utf-8")
-    local = calibration._model_source_fingerprint(str(tmp_path), None)
+    local = calibration.model_source_fingerprint(str(tmp_path), None)
     assert local.startswith("local-manifest:")
     (tmp_path / "model.safetensors").write_bytes(b"0123")
-    assert calibration._model_source_fingerprint(str(tmp_path), None) != local
+    assert calibration.model_source_fingerprint(str(tmp_path), None) != local
 
 
 def test_plugin_generated_artifact_rejects_a_different_model_source(tmp_path: Path) -> None:
@@ -175,7 +175,7 @@ def test_plugin_generated_artifact_rejects_a_different_model_source(tmp_path: Pa
                 "generator": calibration.GENERATOR,
                 "model": "model/a",
                 "model_revision": "default",
-                "model_source_fingerprint": calibration._model_source_fingerprint("model/a", None),
+                "model_source_fingerprint": calibration.model_source_fingerprint("model/a", None),
                 "model_type": "qwen2",
                 "num_layers": 2,
                 "num_attention_heads": 2,
@@ -188,9 +188,55 @@ def test_plugin_generated_artifact_rejects_a_different_model_source(tmp_path: Pa
         output,
     )
     shape = ModelShape("qwen2", 2, 2, 1, 4, 10000.0, False)
-    calibration._validate_artifact(output, shape, SimpleNamespace(model="model/a", revision=None))
+    calibration.validate_artifact(output, shape, SimpleNamespace(model="model/a", revision=None))
     with pytest.raises(ValueError, match="model_source_fingerprint"):
-        calibration._validate_artifact(output, shape, SimpleNamespace(model="model/b", revision=None))
+        calibration.validate_artifact(output, shape, SimpleNamespace(model="model/b", revision=None))
+
+
+@pytest.mark.parametrize("generator, checked", [("kvcompress-mi355x", True), ("vllm-ascend-kvcompress-hust", True), (None, False)])
+def test_provenance_is_checked_for_both_generators(tmp_path: Path, generator, checked) -> None:
+    # Artifacts of this build and of the reference record their model source and
+    # are held to it; an artifact without a generator (e.g. a hand-made or legacy
+    # one) is checked for shape only.
+    output = tmp_path / "stats.pt"
+    metadata = {
+        "model": "model/a",
+        "model_revision": "default",
+        "model_source_fingerprint": calibration.model_source_fingerprint("model/a", None),
+        "model_type": "qwen2",
+    }
+    if generator is not None:
+        metadata["generator"] = generator
+    torch.save({"metadata": metadata, "layer_stats": _layer_stats()}, output)
+    shape = ModelShape("qwen2", 2, 2, 1, 4, 10000.0, False)
+    calibration.validate_artifact(output, shape, SimpleNamespace(model="model/a", revision=None))
+    if checked:
+        with pytest.raises(ValueError, match="calibration model 'model/a' does not match 'model/b'"):
+            calibration.validate_artifact(output, shape, SimpleNamespace(model="model/b", revision=None))
+        with pytest.raises(ValueError, match="model_revision"):
+            calibration.validate_artifact(output, shape, SimpleNamespace(model="model/a", revision="v2"))
+    else:
+        calibration.validate_artifact(output, shape, SimpleNamespace(model="model/b", revision=None))
+
+
+def test_fingerprint_format_is_the_reference_one(tmp_path: Path) -> None:
+    # "identifier:" + sha256("<id>@<revision>") and "local-manifest:" + sha256 of the
+    # compact sorted-key JSON list of [name, size, mtime_ns] (pkg/calibration.py:530-552),
+    # so artifacts validate on either side; computed here from the definition.
+    import hashlib
+    import json
+    import os
+
+    assert calibration.model_source_fingerprint("org/m", "r1") == "identifier:" + hashlib.sha256(b"org/m@r1").hexdigest()
+    for name, data in (("config.json", b"{}"), ("b.safetensors", b"12"), ("a.bin", b"3"), ("notes.txt", b"x")):
+        (tmp_path / name).write_bytes(data)
+    (tmp_path / "sub.bin").mkdir()
+    entries = []
+    for name in sorted(["a.bin", "b.safetensors", "config.json"]):
+        st = os.stat(tmp_path / name)
+        entries.append([name, st.st_size, st.st_mtime_ns])
+    want = "local-manifest:" + hashlib.sha256(json.dumps(entries, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
+    assert calibration.model_source_fingerprint(str(tmp_path), None) == want
 
 
 # ------------------------------------------------------- publish and runner --
@@ -207,8 +253,8 @@ def test_concurrent_generation_publishes_one_atomic_artifact(tmp_path: Path, mon
         time.sleep(0.1)
         return payload
 
-    monkeypatch.setattr(calibration, "_generate_payload", generate)
-    monkeypatch.setattr(calibration, "_validate_existing_for_request", lambda path, request: None)
+    monkeypatch.setattr(calibration, "_artifact", generate)
+    monkeypatch.setattr(calibration, "_validate_for_request", lambda path, request: None)
     with concurrent.futures.ThreadPoolExecutor(max_workers=2) as pool:
         results = list(pool.map(generate_calibration_artifact, (request, request)))
     assert sorted(results) == [False, True]

@@ -117,7 +117,7 @@ def test_qstats_rejects_invalid_arguments(hip_device) -> None:
     from kvcompress_mi355x import _native
 
     acc = calibration.LayerAccumulator()
-    with pytest.raises(RuntimeError, match="width"):
+    with pytest.raises(RuntimeError, match="values per row"):
         acc.add(torch.zeros(4, 10, device=hip_device), 2, 4, 4)
     out = torch.zeros(8, dtype=torch.float64, device=hip_device)
     q = torch.zeros(4, 16, device=hip_device)
@@ -214,7 +214,7 @@ def test_generator_creates_safe_model_matched_artifact(hip_device, tmp_path: Pat
     assert not list(tmp_path.glob("*.tmp"))
     artifact = CalibrationStats.load(output)
     assert artifact.validate(ModelShape("qwen2", 2, 2, 1, 4, 10000.0, False)) == ()
-    assert artifact.metadata["generator"] == "vllm-ascend-kvcompress-hust"
+    assert artifact.metadata["generator"] == calibration.GENERATOR == "kvcompress-mi355x"
     assert artifact.metadata["token_count"] == 32
     assert artifact.metadata["input_source"] == calibration.BUILTIN_INPUT_SOURCE
     assert artifact.layers[0].q_mean_real.shape == (2, 2)
@@ -289,10 +289,10 @@ def test_generator_end_to_end_on_a_local_qwen2_checkpoint(hip_device, tmp_path: 
     )
     assert calibration.generate_calibration_artifact(request)
     artifact = CalibrationStats.load(output)
-    shape = calibration._model_shape_from_hf_config(cfg)
+    shape = calibration.shape_from_hf_config(cfg)
     assert artifact.validate(shape) == ()
     assert artifact.metadata["model_source_fingerprint"].startswith("local-manifest:")
-    calibration._validate_artifact(output, shape, type("M", (), {"model": str(model_dir), "revision": None})())
+    calibration.validate_artifact(output, shape, type("M", (), {"model": str(model_dir), "revision": None})())
 
     # The restatement hooked into the same checkpoint on the CPU.
     reference = transformers.AutoModel.from_pretrained(model_dir, local_files_only=True, dtype=torch.float32,

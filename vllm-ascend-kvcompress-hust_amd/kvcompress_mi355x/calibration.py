@@ -1,42 +1,54 @@
 """Model-matched TriAttention calibration artifacts, accumulated on the GPU.
 
-Counterpart of the reference's generator (pkg/calibration.py): run a Hugging
-Face model once over a calibration text, hook every full-attention layer's
-query projection (``q_norm`` where the attention has one, else ``q_proj``),
-reduce the pre-RoPE queries to per-head statistics and write a schema-3
-artifact that CalibrationStats.load reads:
+The TriAttention scorer needs, per full-attention layer and query head, the
+mean pre-RoPE query of a calibration run (real and imaginary parts per RoPE
+frequency, the mean magnitude per frequency, the mean of the unrotated dims)
+and the rotary frequencies the model itself uses.  This module produces that
+artifact from a Hugging Face checkpoint.
 
-  layer_stats[str(layer)] = {q_mean_real, q_mean_imag, q_abs_mean  [heads, F],
-                             inv_freq [F], freq_scale_sq [1, F],
-                             q_pass_mean [heads, P] (partial RoPE only)}
+How a generation runs (generate_calibration_artifact):
 
-The reduction runs in kvc_qstats_accumulate (one HIP kernel launch per hooked
-projection into a per-layer float64 state on the device, reduced to totals by
-kvc_qstats_finish); a projection produced on the host is copied to the HIP
-device first.  There is no host reduction: without a HIP
-device the generator raises.  Generation takes a file lock next to the output
-and publishes the artifact with an atomic rename, so concurrent workers
-produce one file (pkg/calibration.py:175-193).
+  _OutputLock      exclusive lock on ".<name>.lock" beside the output, so the
+                   workers of one deployment that all find the artifact
+                   missing produce it once; a worker that gets the lock after
+                   the file appeared checks it against its request instead.
+  _Checkpoint      the checkpoint's Hugging Face config, tokenizer and model
+                   (for a multimodal Qwen3.5 checkpoint the causal text model
+                   alone, its weights remapped from model.language_model.*).
+  _DecoderView     the decoder stack inside the loaded model: each
+                   full-attention layer's query module (q_norm where the layer
+                   normalises queries, else q_proj) and its rotary embedding.
+  _QueryCapture    forward hooks that hand every query output to the layer's
+                   LayerAccumulator; one kvc_qstats_accumulate launch per
+                   output sums it into a float64 state on the HIP device.
+  _artifact        means, rotary tables and provenance metadata as a schema-3
+                   payload, read back through CalibrationStats' safe loader
+                   and validator, then written beside the output and renamed
+                   over it (readers never see a partial file).
 
-The request fields, option names, metadata keys, the model-source fingerprint
-and the command-line flags are those of the reference, so artifacts and
-service settings carry over.  The built-in calibration text is this package's
-own (input_source ``builtin:mi355x-systems-v1``); pass ``input_path`` to
-calibrate on a specific text.
+Kept identical to the reference generator (pkg/calibration.py) because other
+tools read or write the same files: the CalibrationRequest fields, the
+command-line flags, the schema-3 layout and metadata keys, and the
+model-source fingerprint ("identifier:" + SHA-256 of "<model>@<revision>", or
+"local-manifest:" + SHA-256 of the checkpoint directory's file manifest), so an
+artifact validates on either side.  Artifacts carry this build's generator
+name; the model-source provenance check applies to artifacts of this
+generator and of the reference's.  The built-in calibration text is this
+package's own (input_source "builtin:mi355x-systems-v1").
 """
 
 from __future__ import annotations
 
 import argparse
 import fcntl
+import fnmatch
 import gc
 import hashlib
 import importlib.util
 import json
 import os
 import tempfile
-from collections.abc import Mapping, Sequence
-from contextlib import suppress
+from collections.abc import Iterator, Mapping, Sequence
 from dataclasses import dataclass
 from datetime import datetime, timezone
 from pathlib import Path
@@ -50,8 +62,13 @@ from .methods.triattention.config import TriAttentionConfig
 from .methods.triattention.stats import SUPPORTED_MODEL_TYPES, CalibrationStats
 from .model import model_shape_from_config
 
-GENERATOR = "vllm-ascend-kvcompress-hust"  # artifact producer name the validators key on
+GENERATOR = "kvcompress-mi355x"
+REFERENCE_GENERATOR = "vllm-ascend-kvcompress-hust"
+# Generators whose artifacts record the model source they were made from.
+PROVENANCE_GENERATORS = frozenset({GENERATOR, REFERENCE_GENERATOR})
 BUILTIN_INPUT_SOURCE = "builtin:mi355x-systems-v1"
+SCHEMA_VERSION = 3
+MIN_MAX_LENGTH = 128
 
 # Built-in calibration text: prose, code, numbers, tables and mixed scripts, so
 # the query statistics see a spread of token kinds.  Repeated with numbered
@@ -91,10 +108,33 @@ reference clock: +38 ms over 24 h. Observations are kept separate from the
 inferred causes, and every value keeps its original unit.""",
 )
 
+# Checkpoint files that identify a local model directory (top level only).
+_MANIFEST_PATTERNS = ("*.safetensors", "*.bin", "*.pt", "*.index.json", "config.json")
+
+_TORCH_DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+_DTYPE_ALIASES = {"half": "float16", "float": "float32", "auto": "bfloat16"}
+
+
+def dtype_name(value: Any) -> str:
+    """Canonical dtype name of a torch dtype or a dtype string ("torch.float16",
+    "half", "auto" -> "float16", "float16", "bfloat16")."""
+    name = str(value).lower().removeprefix("torch.")
+    return _DTYPE_ALIASES.get(name, name)
+
+
+def torch_dtype(value: Any) -> torch.dtype:
+    try:
+        return _TORCH_DTYPES[dtype_name(value)]
+    except KeyError:
+        raise ValueError(f"unsupported calibration dtype: {value}") from None
+
 
 @dataclass(frozen=True)
 class CalibrationRequest:
-    """Generation request (pkg/calibration.py:71-86); ``device`` names a HIP device."""
+    """One artifact to generate (the reference's request fields,
+    pkg/calibration.py:71-86).  ``device`` is where the temporary model runs
+    ("cuda", "cuda:N" or "cpu"); the statistics are always accumulated on a
+    HIP device."""
 
     model: str
     output: Path
@@ -111,9 +151,122 @@ class CalibrationRequest:
     attn_implementation: str = "eager"
     force: bool = False
 
+    @classmethod
+    def for_runner(cls, runner: Any, config: TriAttentionConfig) -> CalibrationRequest:
+        """The request a serving worker makes for its own model: the model
+        config's identity and dtype, the method's calibration options, the
+        worker's device (calibration_device "auto"), and a model spread over
+        the visible devices when the deployment is tensor parallel (the
+        checkpoint then does not fit one device either)."""
+        mc = runner.model_config
+        device = config.calibration_device
+        if device == "auto":
+            device = str(getattr(runner, "device", "cuda"))
+        parallel = getattr(getattr(runner, "vllm_config", None), "parallel_config", None)
+        tp = int(getattr(parallel, "tensor_parallel_size", 1))
+        return cls(
+            model=str(mc.model),
+            output=config.stats_path,
+            input_path=config.calibration_input_path,
+            tokenizer=str(mc.tokenizer) if mc.tokenizer else None,
+            revision=getattr(mc, "revision", None),
+            tokenizer_revision=getattr(mc, "tokenizer_revision", None),
+            trust_remote_code=bool(getattr(mc, "trust_remote_code", False)),
+            local_files_only=config.calibration_local_files_only,
+            max_length=config.calibration_max_length,
+            device=device,
+            device_map="auto" if tp > 1 else None,
+            dtype=dtype_name(getattr(mc, "dtype", "bfloat16")),
+            attn_implementation=config.calibration_attn_implementation,
+        )
+
+
+# -------------------------------------------------------------- provenance --
+
+
+def canonical_digest(value: Any) -> str:
+    """SHA-256 of the canonical JSON form of ``value`` (sorted keys, no spaces,
+    non-JSON values by their str)."""
+    text = json.dumps(value, sort_keys=True, separators=(",", ":"), default=str)
+    return hashlib.sha256(text.encode("utf-8")).hexdigest()
+
+
+def model_source_fingerprint(model: str, revision: str | None) -> str:
+    """Identity of a model source.  A model id: "identifier:" + SHA-256 of
+    "<id>@<revision or default>".  A local checkpoint directory: its top-level
+    checkpoint files (weights, index, config) as (name, size, mtime_ns) in name
+    order, "local-manifest:" + their canonical digest; the weights are not
+    read."""
+    directory = Path(model).expanduser()
+    if not directory.is_dir():
+        return "identifier:" + hashlib.sha256(f"{model}@{revision or 'default'}".encode()).hexdigest()
+    manifest = []
+    for entry in sorted(os.scandir(directory), key=lambda e: e.name):
+        if entry.is_file() and any(fnmatch.fnmatchcase(entry.name, p) for p in _MANIFEST_PATTERNS):
+            info = entry.stat()
+            manifest.append((entry.name, int(info.st_size), int(info.st_mtime_ns)))
+    if not manifest:
+        raise ValueError(f"no checkpoint files (weights, index or config.json) in model directory {directory}")
+    return "local-manifest:" + canonical_digest(manifest)
+
+
+def shape_from_hf_config(hf_config: Any) -> ModelShape:
+    """ModelShape of a Hugging Face config (its text config for multimodal ones)."""
+    return model_shape_from_config(_HostModelConfig(hf_text_config=getattr(hf_config, "text_config", hf_config)))
+
+
+@dataclass(frozen=True)
+class _HostModelConfig:
+    """The parts of a serving host's model config the checks read."""
+
+    hf_text_config: Any = None
+    model: str = ""
+    revision: str | None = None
+
+
+def rope_type_of(hf_config: Any) -> str:
+    """RoPE type named by rope_parameters (or rope_scaling), "default" if none."""
+    text = getattr(hf_config, "text_config", hf_config)
+    for entry in (getattr(text, "rope_parameters", None), getattr(text, "rope_scaling", None)):
+        if isinstance(entry, Mapping):
+            return str(entry.get("rope_type", entry.get("type", "default")) or "default")
+    return "default"
+
+
+# -------------------------------------------------------------------- text --
+
+
+def calibration_text(request: CalibrationRequest) -> tuple[str, str]:
+    """(text, input_source): the request's file, or the built-in sections
+    repeated under numbered headings to about six characters per requested
+    token (the tokenizer truncates to max_length)."""
+    if request.input_path is not None:
+        path = request.input_path.expanduser().resolve()
+        if not path.is_file():
+            raise ValueError(f"calibration input file does not exist: {path}")
+        text = path.read_text(encoding="utf-8")
+        if not text.strip():
+            raise ValueError(f"calibration input file is empty: {path}")
+        return text, str(path)
+    wanted = 6 * request.max_length
+    parts: list[str] = []
+    size = 0
+    repeat = 0
+    while size < wanted:
+        repeat += 1
+        for number, section in enumerate(_BUILTIN_SECTIONS, 1):
+            part = f"Part {repeat}.{number}\n{section}\n"
+            parts.append(part)
+            size += len(part)
+    return "\n".join(parts), BUILTIN_INPUT_SOURCE
+
+
+# ------------------------------------------------------------ accumulation --
+
 
 def _hip_device(device: torch.device | str | None) -> torch.device:
-    """The HIP device the statistics are accumulated on."""
+    """The HIP device the statistics are accumulated on (the current one when
+    the model itself runs elsewhere)."""
     if not torch.cuda.is_available():
         raise RuntimeError("calibration statistics are accumulated on a HIP device; none is available")
     dev = torch.device("cuda") if device is None else torch.device(device)
@@ -131,7 +284,8 @@ def _kernel_dtype(dtype: torch.dtype) -> int:
 
 
 class LayerAccumulator:
-    """Running query sums of one layer (_LayerAccumulator, pkg/calibration.py:89-131).
+    """Running query sums of one layer (the reference's _LayerAccumulator,
+    pkg/calibration.py:89-131).
 
     ``add`` takes a hooked projection: the query part of ``q_proj``'s output
     ([..., heads*head_dim], or twice that when the projection carries an
@@ -162,8 +316,8 @@ class LayerAccumulator:
             or (projected.shape[-1] == head_dim and projected.numel() % expected == 0)
         ):
             raise RuntimeError(
-                "query projection width does not match model attention shape: "
-                f"got {projected.shape[-1]}, expected {expected}"
+                f"hooked query output has {projected.shape[-1]} values per row; the attention shape "
+                f"({heads} heads x {head_dim}) needs {expected} (or {2 * expected} with an output gate)"
             )
         if self._shape is None:
             self._shape = (heads, head_dim, rotary_dim)
@@ -260,469 +414,424 @@ class LayerAccumulator:
         return out
 
 
-# ------------------------------------------------------------------ runner --
+# ------------------------------------------------------------------- model --
+
+_WRAPPER_ATTRIBUTES = ("model", "language_model", "text_model")
 
 
-def ensure_calibration_for_runner(runner: Any, selection: Any) -> bool:
-    """Generate a missing artifact before the serving weights load
-    (pkg/calibration.py:134-172); True when this call generated it."""
-    if getattr(selection, "method", None) != "triattention":
-        return False
-    config = TriAttentionConfig.from_method_config(selection.method_config)
-    model_config = runner.model_config
-    shape = model_shape_from_config(model_config)
-    if config.stats_path.is_file():
-        _validate_artifact(config.stats_path, shape, model_config)
-        return False
-    if not config.auto_calibrate:
-        return False
-    device = (
-        str(getattr(runner, "device", "cuda")) if config.calibration_device == "auto" else config.calibration_device
-    )
-    parallel = getattr(getattr(runner, "vllm_config", None), "parallel_config", None)
-    tensor_parallel = int(getattr(parallel, "tensor_parallel_size", 1))
-    request = CalibrationRequest(
-        model=str(model_config.model),
-        tokenizer=str(model_config.tokenizer) if model_config.tokenizer else None,
-        output=config.stats_path,
-        input_path=config.calibration_input_path,
-        revision=getattr(model_config, "revision", None),
-        tokenizer_revision=getattr(model_config, "tokenizer_revision", None),
-        trust_remote_code=bool(getattr(model_config, "trust_remote_code", False)),
-        local_files_only=config.calibration_local_files_only,
-        max_length=config.calibration_max_length,
-        device=device,
-        # A model sharded for tensor parallelism does not fit one device either.
-        device_map="auto" if tensor_parallel > 1 else None,
-        dtype=_dtype_name(getattr(model_config, "dtype", "bfloat16")),
-        attn_implementation=config.calibration_attn_implementation,
-    )
-    generated = generate_calibration_artifact(request)
-    _validate_artifact(config.stats_path, shape, model_config)
-    return generated
+class _DecoderView:
+    """The decoder stack inside a loaded model and its attention layers.
 
+    The stack is the shallowest module holding a ``layers`` ModuleList,
+    searched level by level through the usual wrapper attributes (a causal-LM
+    head's ``model``, a multimodal model's ``language_model`` / ``text_model``).
+    Every layer with a ``self_attn`` module is a full-attention layer; hybrid
+    models' linear-attention layers have none."""
 
-def generate_calibration_artifact(request: CalibrationRequest) -> bool:
-    """Generate one artifact; False when it already exists (another process won)."""
-    if request.max_length < 128:
-        raise ValueError("calibration max_length must be at least 128")
-    output = request.output.expanduser().resolve()
-    output.parent.mkdir(parents=True, exist_ok=True)
-    with output.with_name(f".{output.name}.lock").open("a+b") as lock:
-        fcntl.flock(lock.fileno(), fcntl.LOCK_EX)
-        if output.is_file() and not request.force:
-            _validate_existing_for_request(output, request)
-            return False
-        _atomic_torch_save(_generate_payload(request), output)
-    return True
+    def __init__(self, model: torch.nn.Module) -> None:
+        self.stack = self._find_stack(model)
+        self.attention = [
+            (index, layer.self_attn)
+            for index, layer in enumerate(self.stack.layers)
+            if isinstance(getattr(layer, "self_attn", None), torch.nn.Module)
+        ]
 
+    @staticmethod
+    def _find_stack(model: torch.nn.Module) -> torch.nn.Module:
+        level: list[torch.nn.Module] = [model]
+        visited: set[int] = set()
+        while level:
+            for module in level:
+                if isinstance(getattr(module, "layers", None), torch.nn.ModuleList):
+                    return module
+            visited.update(id(m) for m in level)
+            level = [
+                child
+                for module in level
+                for child in (getattr(module, name, None) for name in _WRAPPER_ATTRIBUTES)
+                if isinstance(child, torch.nn.Module) and id(child) not in visited
+            ]
+        raise RuntimeError("no decoder layer stack found in the calibration model")
 
-def _generate_payload(request: CalibrationRequest) -> dict[str, Any]:
-    if request.device_map is not None and importlib.util.find_spec("accelerate") is None:
-        raise RuntimeError(
-            "distributed calibration requires Accelerate; install the "
-            "'vllm-ascend-kvcompress-hust[calibration]' extra in the host environment"
-        )
-    try:
-        from transformers import AutoConfig, AutoModel, AutoModelForCausalLM, AutoTokenizer
-        from transformers import __version__ as transformers_version
-    except ImportError as error:
-        raise RuntimeError("calibration generation requires the Transformers package") from error
+    @property
+    def layer_indices(self) -> tuple[int, ...]:
+        return tuple(index for index, _ in self.attention)
 
-    _prepare_device(request.device)
-    accumulate_on = _hip_device(request.device)
-    input_device = torch.device("cpu" if request.device_map == "auto" else request.device)
-    common = {"trust_remote_code": request.trust_remote_code, "local_files_only": request.local_files_only}
-    config = AutoConfig.from_pretrained(request.model, revision=request.revision, **common)
-    shape = _model_shape_from_hf_config(config)
-    if shape.model_type not in SUPPORTED_MODEL_TYPES:
-        raise ValueError(f"model_type {shape.model_type!r} is not supported for calibration")
-    tokenizer_id = request.tokenizer or request.model
-    tokenizer = AutoTokenizer.from_pretrained(
-        tokenizer_id, revision=request.tokenizer_revision or request.revision, **common
-    )
-    text, input_source = _load_calibration_text(request)
-    encoded = tokenizer(
-        text, return_tensors="pt", truncation=True, max_length=request.max_length, add_special_tokens=True
-    )
-    input_ids = encoded.get("input_ids")
-    if not isinstance(input_ids, torch.Tensor) or input_ids.ndim != 2:
-        raise RuntimeError("tokenizer did not return rank-two input_ids")
-    token_count = int(input_ids.shape[1])
-    if token_count < 2:
-        raise ValueError("calibration input produced fewer than two tokens")
-
-    text_config = getattr(config, "text_config", config)
-    multimodal_qwen35 = text_config is not config and str(getattr(config, "model_type", "")).startswith("qwen3_5")
-    options: dict[str, Any] = {
-        "config": text_config if multimodal_qwen35 else config,
-        "revision": request.revision,
-        "dtype": _torch_dtype(request.dtype),
-        "device_map": request.device_map or request.device,
-        **common,
-    }
-    if request.attn_implementation:
-        options["attn_implementation"] = request.attn_implementation
-    if multimodal_qwen35:
-        # The published checkpoint nests the text weights under model.language_model;
-        # loading the causal text model alone skips the vision tower.
-        options["key_mapping"] = {r"^model\.language_model\.(.+)$": r"model.\1"}
-
-    model: torch.nn.Module | None = None
-    handles: list[Any] = []
-    try:
-        loader = AutoModelForCausalLM if multimodal_qwen35 else AutoModel
-        model = loader.from_pretrained(request.model, **options)
-        model.eval()
-        attention_layers = _find_attention_layers(model)
-        found = tuple(index for index, _ in attention_layers)
-        if found != shape.full_attention_layer_indices:
-            raise RuntimeError(
-                f"located full-attention layers do not match model config: got {found}, "
-                f"expected {shape.full_attention_layer_indices}"
+    def query_modules(self) -> Iterator[tuple[int, torch.nn.Module]]:
+        """(layer, module whose output is the layer's pre-RoPE query)."""
+        for index, attention in self.attention:
+            module = next(
+                (m for m in (getattr(attention, "q_norm", None), getattr(attention, "q_proj", None))
+                 if isinstance(m, torch.nn.Module)),
+                None,
             )
-        accumulators = {index: LayerAccumulator(device=accumulate_on) for index, _ in attention_layers}
-        for index, attention in attention_layers:
-            module = getattr(attention, "q_norm", None)
-            if not isinstance(module, torch.nn.Module):
-                module = getattr(attention, "q_proj", None)
-            if not isinstance(module, torch.nn.Module):
-                raise RuntimeError(f"attention layer {index} exposes neither q_norm nor q_proj")
+            if module is None:
+                raise RuntimeError(f"attention layer {index} has neither a q_norm nor a q_proj module to observe")
+            yield index, module
 
-            def capture(_module: torch.nn.Module, _inputs: tuple[Any, ...], output: Any, *, layer: int = index) -> None:
-                if not isinstance(output, torch.Tensor):
-                    raise RuntimeError(f"attention layer {layer} q_proj returned a non-tensor")
-                accumulators[layer].add(output, shape.num_attention_heads, shape.head_dim, shape.effective_rotary_dim)
+    def rotary_tables(self, shape: ModelShape, rope_type: str) -> dict[int, tuple[torch.Tensor, torch.Tensor]]:
+        """(inv_freq [F], freq_scale_sq [1, F]) per attention layer from the
+        rotary embedding the layer uses (its own, else the stack's shared one):
+        its exact inverse frequencies (the theta default for unscaled RoPE
+        when the module exposes none) and the square of its attention scaling
+        (a scalar, or per frequency, or per dim of which the first F count)."""
+        shared = getattr(self.stack, "rotary_emb", None)
+        freq = shape.effective_rotary_dim // 2
+        tables = {}
+        for index, attention in self.attention:
+            rotary = getattr(attention, "rotary_emb", shared)
+            inv_freq = getattr(rotary, "inv_freq", None)
+            if isinstance(inv_freq, torch.Tensor):
+                inv_freq = inv_freq.detach().to("cpu", torch.float32).reshape(-1)
+            elif rope_type == "default":
+                steps = torch.arange(0, shape.effective_rotary_dim, 2, dtype=torch.float32)
+                inv_freq = 1.0 / (shape.rope_theta ** (steps / shape.effective_rotary_dim))
+            else:
+                raise RuntimeError(f"layer {index} uses {rope_type!r} RoPE but exposes no exact inv_freq")
+            if inv_freq.numel() != freq:
+                raise RuntimeError(f"layer {index} inv_freq has {inv_freq.numel()} values; expected {freq}")
+            scaling = torch.as_tensor(getattr(rotary, "attention_scaling", 1.0), dtype=torch.float32).cpu().reshape(-1)
+            if scaling.numel() == 1:
+                scaling = scaling.repeat(freq)
+            elif scaling.numel() in (shape.head_dim, shape.effective_rotary_dim):
+                scaling = scaling[:freq]
+            elif scaling.numel() != freq:
+                raise RuntimeError(f"layer {index} attention scaling has {scaling.numel()} values")
+            tables[index] = (inv_freq.contiguous(), scaling.square().reshape(1, freq).contiguous())
+        return tables
 
-            handles.append(module.register_forward_hook(capture))
 
-        inputs = {name: value.to(input_device) for name, value in encoded.items() if isinstance(value, torch.Tensor)}
-        with torch.inference_mode():
-            model(**inputs, use_cache=False)
-        torch.cuda.synchronize(accumulate_on)
+class _QueryCapture:
+    """Forward hooks from every attention layer's query module into that
+    layer's LayerAccumulator, removed on exit."""
 
-        rope_type = _rope_type(config)
-        rope_values = _extract_rope_values(model, attention_layers, shape, rope_type)
-        layer_stats: dict[str, dict[str, torch.Tensor]] = {}
-        for index, accumulator in accumulators.items():
-            if accumulator.count <= 0:
-                raise RuntimeError(f"no query values captured for layer {index}")
-            inv_freq, freq_scale_sq = rope_values[index]
-            values = accumulator.means()
-            values["inv_freq"] = inv_freq
-            values["freq_scale_sq"] = freq_scale_sq
-            layer_stats[str(index)] = values
+    def __init__(self, decoder: _DecoderView, shape: ModelShape, device: torch.device) -> None:
+        self.decoder = decoder
+        self.shape = shape
+        self.accumulators = {index: LayerAccumulator(device=device) for index in decoder.layer_indices}
+        self._handles: list[Any] = []
 
-        config_dict = config.to_dict() if hasattr(config, "to_dict") else vars(config)
-        metadata = {
-            "schema_version": 3,
-            "generator": GENERATOR,
-            "generator_version": __version__,
-            "accumulator": "kvc_qstats_accumulate (float64 sums, HIP)",
-            "transformers_version": transformers_version,
-            "created_at_utc": datetime.now(timezone.utc).isoformat(),
-            "model": request.model,
-            "model_revision": request.revision or "default",
-            "model_source_fingerprint": _model_source_fingerprint(request.model, request.revision),
-            "tokenizer": tokenizer_id,
-            "tokenizer_revision": request.tokenizer_revision or request.revision or "default",
-            "model_config_sha256": _sha256_json(config_dict),
-            "input_source": input_source,
-            "input_sha256": hashlib.sha256(text.encode("utf-8")).hexdigest(),
-            "token_count": token_count,
-            "requested_max_length": request.max_length,
-            "num_traces": 1,
-            "model_type": shape.model_type,
-            "num_layers": shape.num_layers,
-            "num_attention_heads": shape.num_attention_heads,
-            "num_kv_heads": shape.num_kv_heads,
-            "head_dim": shape.head_dim,
-            "rotary_dim": shape.effective_rotary_dim,
-            "attention_layer_indices": list(shape.full_attention_layer_indices),
-            "rope_theta": shape.rope_theta,
-            "rope_style": "half",
-            "rope_type": rope_type,
-            "dtype": request.dtype,
-            "attn_implementation": request.attn_implementation,
+    def _hook(self, index: int):
+        acc, shape = self.accumulators[index], self.shape
+
+        def observe(_module: torch.nn.Module, _args: tuple[Any, ...], output: Any) -> None:
+            if not isinstance(output, torch.Tensor):
+                raise RuntimeError(f"query module of attention layer {index} returned {type(output).__name__}, not a tensor")
+            acc.add(output, shape.num_attention_heads, shape.head_dim, shape.effective_rotary_dim)
+
+        return observe
+
+    def __enter__(self) -> _QueryCapture:
+        for index, module in self.decoder.query_modules():
+            self._handles.append(module.register_forward_hook(self._hook(index)))
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        while self._handles:
+            self._handles.pop().remove()
+
+
+class _Checkpoint:
+    """A request's Hugging Face config, tokenizer and (on demand) model."""
+
+    def __init__(self, request: CalibrationRequest) -> None:
+        if request.device_map is not None and importlib.util.find_spec("accelerate") is None:
+            raise RuntimeError(
+                "device_map='auto' spreads the calibration model with the accelerate package, which this "
+                "environment lacks (the package's [calibration] extra provides it)"
+            )
+        try:
+            import transformers
+        except ImportError as error:
+            raise RuntimeError("calibration generation requires the Transformers package") from error
+        if str(request.device).startswith("npu"):
+            raise RuntimeError("calibration runs on HIP devices ('cuda' in torch); 'npu' is not available")
+        self.request = request
+        self.transformers = transformers
+        self.loader_options = {"trust_remote_code": request.trust_remote_code, "local_files_only": request.local_files_only}
+        self.config = transformers.AutoConfig.from_pretrained(request.model, revision=request.revision, **self.loader_options)
+        self.shape = shape_from_hf_config(self.config)
+        if self.shape.model_type not in SUPPORTED_MODEL_TYPES:
+            raise ValueError(f"model_type {self.shape.model_type!r} is not supported for calibration")
+        self.tokenizer_id = request.tokenizer or request.model
+        self.tokenizer = transformers.AutoTokenizer.from_pretrained(
+            self.tokenizer_id, revision=request.tokenizer_revision or request.revision, **self.loader_options
+        )
+
+    @property
+    def text_only_multimodal(self) -> bool:
+        """A multimodal Qwen3.5 checkpoint, calibrated through its causal text model."""
+        text = getattr(self.config, "text_config", self.config)
+        return text is not self.config and str(getattr(self.config, "model_type", "")).startswith("qwen3_5")
+
+    def encode(self, text: str) -> dict[str, torch.Tensor]:
+        encoded = self.tokenizer(
+            text, return_tensors="pt", truncation=True, max_length=self.request.max_length, add_special_tokens=True
+        )
+        ids = encoded.get("input_ids")
+        if not isinstance(ids, torch.Tensor) or ids.ndim != 2:
+            raise RuntimeError("the tokenizer returned no [batch, tokens] input_ids tensor")
+        if ids.shape[1] < 2:
+            raise ValueError("calibration input produced fewer than two tokens")
+        return {name: value for name, value in encoded.items() if isinstance(value, torch.Tensor)}
+
+    def load_model(self) -> torch.nn.Module:
+        request, tf = self.request, self.transformers
+        options: dict[str, Any] = {
+            "revision": request.revision,
+            "dtype": torch_dtype(request.dtype),
+            "device_map": request.device_map or request.device,
+            **self.loader_options,
         }
-        payload = {"metadata": metadata, "layer_stats": layer_stats}
-        reasons = _load_payload(payload).validate(shape)
-        if reasons:
-            raise ValueError("generated calibration is incompatible: " + "; ".join(reasons))
-        return payload
+        if request.attn_implementation:
+            options["attn_implementation"] = request.attn_implementation
+        if self.text_only_multimodal:
+            # Text weights sit under model.language_model.* in the multimodal
+            # checkpoint; the causal text model expects them under model.*.
+            options["config"] = self.config.text_config
+            options["key_mapping"] = {r"^model\.language_model\.(.+)$": r"model.\1"}
+            model = tf.AutoModelForCausalLM.from_pretrained(request.model, **options)
+        else:
+            options["config"] = self.config
+            model = tf.AutoModel.from_pretrained(request.model, **options)
+        return model.eval()
+
+
+def _release_device_memory(request: CalibrationRequest) -> None:
+    if not torch.cuda.is_available():
+        return
+    devices = range(torch.cuda.device_count()) if request.device_map == "auto" else (torch.cuda.current_device(),)
+    for index in devices:
+        with torch.cuda.device(index):
+            torch.cuda.empty_cache()
+
+
+def _artifact(request: CalibrationRequest) -> dict[str, Any]:
+    """The schema-3 payload of one calibration run over the request's text."""
+    checkpoint = _Checkpoint(request)
+    shape = checkpoint.shape
+    text, input_source = calibration_text(request)
+    inputs = checkpoint.encode(text)
+    token_count = int(inputs["input_ids"].shape[1])
+    input_device = torch.device("cpu" if request.device_map == "auto" else request.device)
+    accumulate_on = _hip_device(request.device)
+    rope_type = rope_type_of(checkpoint.config)
+
+    model = None
+    try:
+        model = checkpoint.load_model()
+        decoder = _DecoderView(model)
+        if decoder.layer_indices != shape.full_attention_layer_indices:
+            raise RuntimeError(
+                f"the model's attention layers {decoder.layer_indices} differ from the config's full-attention "
+                f"layers {shape.full_attention_layer_indices}"
+            )
+        with _QueryCapture(decoder, shape, accumulate_on) as capture, torch.inference_mode():
+            model(**{name: value.to(input_device) for name, value in inputs.items()}, use_cache=False)
+        torch.cuda.synchronize(accumulate_on)
+        rotary = decoder.rotary_tables(shape, rope_type)
+        layer_stats = {}
+        for index, acc in capture.accumulators.items():
+            if acc.count <= 0:
+                raise RuntimeError(f"the forward pass produced no queries for attention layer {index}")
+            inv_freq, freq_scale_sq = rotary[index]
+            layer_stats[str(index)] = {**acc.means(), "inv_freq": inv_freq, "freq_scale_sq": freq_scale_sq}
     finally:
-        for handle in handles:
-            handle.remove()
         del model
         gc.collect()
-        _empty_device_cache(request.device, all_devices=request.device_map == "auto")
+        _release_device_memory(request)
+
+    hf_dict = checkpoint.config.to_dict() if hasattr(checkpoint.config, "to_dict") else vars(checkpoint.config)
+    metadata = {
+        # provenance
+        "schema_version": SCHEMA_VERSION,
+        "generator": GENERATOR,
+        "generator_version": __version__,
+        "accumulator": "kvc_qstats_accumulate (float64 sums, HIP)",
+        "transformers_version": checkpoint.transformers.__version__,
+        "created_at_utc": datetime.now(timezone.utc).isoformat(),
+        "model": request.model,
+        "model_revision": request.revision or "default",
+        "model_source_fingerprint": model_source_fingerprint(request.model, request.revision),
+        "tokenizer": checkpoint.tokenizer_id,
+        "tokenizer_revision": request.tokenizer_revision or request.revision or "default",
+        "model_config_sha256": canonical_digest(hf_dict),
+        # calibration input
+        "input_source": input_source,
+        "input_sha256": hashlib.sha256(text.encode("utf-8")).hexdigest(),
+        "token_count": token_count,
+        "requested_max_length": request.max_length,
+        "num_traces": 1,
+        # model shape the statistics belong to
+        "model_type": shape.model_type,
+        "num_layers": shape.num_layers,
+        "num_attention_heads": shape.num_attention_heads,
+        "num_kv_heads": shape.num_kv_heads,
+        "head_dim": shape.head_dim,
+        "rotary_dim": shape.effective_rotary_dim,
+        "attention_layer_indices": list(shape.full_attention_layer_indices),
+        "rope_theta": shape.rope_theta,
+        "rope_style": "half",
+        "rope_type": rope_type,
+        "dtype": request.dtype,
+        "attn_implementation": request.attn_implementation,
+    }
+    payload = {"metadata": metadata, "layer_stats": layer_stats}
+    problems = _round_trip(payload).validate(shape)
+    if problems:
+        raise ValueError("the generated calibration does not fit its own model: " + "; ".join(problems))
+    return payload
 
 
-# --------------------------------------------------------------- artifacts --
+# -------------------------------------------------------------- validation --
 
 
-def _load_payload(payload: Mapping[str, Any]) -> CalibrationStats:
-    """Read a payload back through the safe loader and validator."""
-    handle, raw = tempfile.mkstemp(suffix=".pt")
-    os.close(handle)
-    path = Path(raw)
-    try:
+def _round_trip(payload: Mapping[str, Any]) -> CalibrationStats:
+    """The payload as the safe loader reads it back from disk."""
+    with tempfile.TemporaryDirectory() as scratch:
+        path = Path(scratch) / "payload.pt"
         torch.save(dict(payload), path)
         return CalibrationStats.load(path)
-    finally:
-        path.unlink(missing_ok=True)
 
 
-def _validate_artifact(path: Path, shape: ModelShape, model_config: Any | None = None) -> None:
+def validate_artifact(path: Path, shape: ModelShape, model_config: Any | None = None) -> None:
+    """Raise ValueError unless the artifact at ``path`` fits ``shape`` and, for
+    an artifact whose generator records its model source, comes from
+    ``model_config``'s model (id, revision and source fingerprint)."""
     artifact = CalibrationStats.load(path)
-    reasons = list(artifact.validate(shape))
-    if model_config is not None and artifact.metadata.get("generator") == GENERATOR:
-        model = str(model_config.model)
-        revision = getattr(model_config, "revision", None)
-        expected = {
-            "model": model,
-            "model_revision": revision or "default",
-            "model_source_fingerprint": _model_source_fingerprint(model, revision),
-        }
-        for key, want in expected.items():
-            got = artifact.metadata.get(key)
-            if got != want:
-                reasons.append(f"calibration {key} {got!r} does not match {want!r}")
-    if reasons:
-        raise ValueError(f"calibration artifact {path} is incompatible: " + "; ".join(reasons))
+    problems = list(artifact.validate(shape))
+    md = artifact.metadata
+    if model_config is not None and md.get("generator") in PROVENANCE_GENERATORS:
+        model, revision = str(model_config.model), getattr(model_config, "revision", None)
+        for key, want in (
+            ("model", model),
+            ("model_revision", revision or "default"),
+            ("model_source_fingerprint", model_source_fingerprint(model, revision)),
+        ):
+            if md.get(key) != want:
+                problems.append(f"calibration {key} {md.get(key)!r} does not match {want!r}")
+    if problems:
+        raise ValueError(f"calibration artifact {path} is incompatible: " + "; ".join(problems))
 
 
-def _validate_existing_for_request(path: Path, request: CalibrationRequest) -> None:
+def _validate_for_request(path: Path, request: CalibrationRequest) -> None:
+    """Check an artifact another worker published against this request's model."""
     try:
         from transformers import AutoConfig
     except ImportError as error:
         raise RuntimeError("calibration validation requires the Transformers package") from error
-    config = AutoConfig.from_pretrained(
+    hf_config = AutoConfig.from_pretrained(
         request.model,
         revision=request.revision,
         trust_remote_code=request.trust_remote_code,
         local_files_only=request.local_files_only,
     )
-    model_config = type("ModelConfig", (), {"model": request.model, "revision": request.revision})()
-    _validate_artifact(path, _model_shape_from_hf_config(config), model_config)
+    validate_artifact(path, shape_from_hf_config(hf_config), _HostModelConfig(model=request.model, revision=request.revision))
 
 
-def _atomic_torch_save(payload: Mapping[str, Any], output: Path) -> None:
-    """Write next to ``output``, flush to disk, then rename over it."""
-    descriptor, raw = tempfile.mkstemp(prefix=f".{output.name}.", suffix=".tmp", dir=output.parent)
-    temporary = Path(raw)
-    try:
-        with os.fdopen(descriptor, "wb") as stream:
-            torch.save(dict(payload), stream)
-            stream.flush()
-            os.fsync(stream.fileno())
-        os.replace(temporary, output)
-    except Exception:
-        with suppress(OSError):
-            os.close(descriptor)
-        temporary.unlink(missing_ok=True)
-        raise
+# --------------------------------------------------------------- publishing --
 
 
-# ------------------------------------------------------------ model walking --
+class _OutputLock:
+    """Exclusive flock on ".<output name>.lock" beside the output for the span
+    of one generation; ``publish`` writes a payload next to the output, syncs
+    it and renames it over the output."""
+
+    def __init__(self, output: Path) -> None:
+        self.output = output
+        self._lock_file = None
+
+    def __enter__(self) -> _OutputLock:
+        self.output.parent.mkdir(parents=True, exist_ok=True)
+        self._lock_file = open(self.output.with_name(f".{self.output.name}.lock"), "a+b")  # noqa: SIM115
+        fcntl.flock(self._lock_file.fileno(), fcntl.LOCK_EX)
+        return self
+
+    def __exit__(self, *exc: object) -> None:
+        if self._lock_file is not None:
+            fcntl.flock(self._lock_file.fileno(), fcntl.LOCK_UN)
+            self._lock_file.close()
+            self._lock_file = None
+
+    def publish(self, payload: Mapping[str, Any]) -> None:
+        staged = tempfile.NamedTemporaryFile(
+            prefix=f".{self.output.name}.", suffix=".tmp", dir=self.output.parent, delete=False
+        )
+        try:
+            with staged:
+                torch.save(dict(payload), staged)
+                staged.flush()
+                os.fsync(staged.fileno())
+            os.replace(staged.name, self.output)
+        except BaseException:
+            Path(staged.name).unlink(missing_ok=True)
+            raise
 
 
-def _find_transformer_backbone(model: torch.nn.Module) -> torch.nn.Module:
-    """Breadth-first through ``model`` / ``language_model`` / ``text_model``
-    wrappers to the module that holds the decoder ``layers``."""
-    queue: list[torch.nn.Module] = [model]
-    seen: set[int] = set()
-    while queue:
-        candidate = queue.pop(0)
-        if id(candidate) in seen:
-            continue
-        seen.add(id(candidate))
-        if isinstance(getattr(candidate, "layers", None), torch.nn.ModuleList):
-            return candidate
-        for name in ("model", "language_model", "text_model"):
-            child = getattr(candidate, name, None)
-            if isinstance(child, torch.nn.Module):
-                queue.append(child)
-    raise RuntimeError("cannot locate transformer decoder layers")
+# ------------------------------------------------------------ entry points --
 
 
-def _find_attention_layers(model: torch.nn.Module) -> list[tuple[int, torch.nn.Module]]:
-    layers = _find_transformer_backbone(model).layers
-    return [
-        (index, layer.self_attn)
-        for index, layer in enumerate(list(layers))
-        if isinstance(getattr(layer, "self_attn", None), torch.nn.Module)
-    ]
+def generate_calibration_artifact(request: CalibrationRequest) -> bool:
+    """Generate the request's artifact.  False when the output already exists
+    (generated by another worker while this one waited for the lock, or
+    before; it is validated against the request) and ``force`` is not set."""
+    if request.max_length < MIN_MAX_LENGTH:
+        raise ValueError(f"calibration max_length must be at least {MIN_MAX_LENGTH}")
+    output = request.output.expanduser().resolve()
+    with _OutputLock(output) as lock:
+        if output.is_file() and not request.force:
+            _validate_for_request(output, request)
+            return False
+        lock.publish(_artifact(request))
+    return True
 
 
-def _extract_rope_values(
-    model: torch.nn.Module,
-    attention_layers: Sequence[tuple[int, torch.nn.Module]],
-    shape: ModelShape,
-    rope_type: str,
-) -> dict[int, tuple[torch.Tensor, torch.Tensor]]:
-    """(inv_freq [F], freq_scale_sq [1, F]) per layer from the model's rotary
-    embedding: the layer's own, else the backbone's shared one."""
-    shared = getattr(_find_transformer_backbone(model), "rotary_emb", None)
-    freq = shape.effective_rotary_dim // 2
-    values: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
-    for index, attention in attention_layers:
-        rotary = getattr(attention, "rotary_emb", shared)
-        inv_freq = getattr(rotary, "inv_freq", None)
-        if isinstance(inv_freq, torch.Tensor):
-            inv_freq = inv_freq.detach().float().cpu().flatten()
-        elif rope_type == "default":
-            exponents = torch.arange(0, shape.effective_rotary_dim, 2, dtype=torch.float32)
-            inv_freq = 1.0 / (shape.rope_theta ** (exponents / shape.effective_rotary_dim))
-        else:
-            raise RuntimeError(f"scaled RoPE layer {index} does not expose exact inv_freq")
-        if inv_freq.numel() != freq:
-            raise RuntimeError(f"layer {index} inv_freq has {inv_freq.numel()} values; expected {freq}")
-        scale = torch.as_tensor(getattr(rotary, "attention_scaling", 1.0), dtype=torch.float32).cpu().flatten()
-        if scale.numel() == 1:
-            scale = scale.expand(freq)
-        elif scale.numel() in {shape.head_dim, shape.effective_rotary_dim}:
-            scale = scale[:freq]
-        elif scale.numel() != freq:
-            raise RuntimeError(f"layer {index} attention scaling has {scale.numel()} values")
-        values[index] = (inv_freq.contiguous(), scale.square().unsqueeze(0).contiguous())
-    return values
+def ensure_calibration_for_runner(runner: Any, selection: Any) -> bool:
+    """Serving-startup hook (called before the serving weights load, so the
+    temporary calibration model is gone by then): for a TriAttention selection
+    whose statistics file is missing and auto_calibrate is on, generate it for
+    the runner's model; an existing file is validated against the model.
+    True when this call generated the artifact."""
+    if getattr(selection, "method", None) != "triattention":
+        return False
+    config = TriAttentionConfig.from_method_config(selection.method_config)
+    shape = model_shape_from_config(runner.model_config)
+    if not config.stats_path.is_file():
+        if not config.auto_calibrate:
+            return False
+        generated = generate_calibration_artifact(CalibrationRequest.for_runner(runner, config))
+    else:
+        generated = False
+    validate_artifact(config.stats_path, shape, runner.model_config)
+    return generated
 
 
-def _model_shape_from_hf_config(config: Any) -> ModelShape:
-    holder = type("ModelConfig", (), {"hf_text_config": getattr(config, "text_config", config)})()
-    return model_shape_from_config(holder)
-
-
-def _rope_type(config: Any) -> str:
-    config = getattr(config, "text_config", config)
-    parameters = getattr(config, "rope_parameters", None)
-    raw = parameters if isinstance(parameters, Mapping) else getattr(config, "rope_scaling", None)
-    if isinstance(raw, Mapping):
-        return str(raw.get("rope_type", raw.get("type", "default")) or "default")
-    return "default"
-
-
-# ------------------------------------------------------------------ inputs --
-
-
-def _load_calibration_text(request: CalibrationRequest) -> tuple[str, str]:
-    """(text, input_source): the request's file, or the built-in text repeated
-    to about six characters per requested token."""
-    if request.input_path is not None:
-        path = request.input_path.expanduser().resolve()
-        if not path.is_file():
-            raise ValueError(f"calibration input file does not exist: {path}")
-        text = path.read_text(encoding="utf-8")
-        if not text.strip():
-            raise ValueError(f"calibration input file is empty: {path}")
-        return text, str(path)
-    target = request.max_length * 6
-    blocks: list[str] = []
-    length = 0
-    round_index = 0
-    while length < target:
-        round_index += 1
-        for section_index, section in enumerate(_BUILTIN_SECTIONS, 1):
-            block = f"Part {round_index}.{section_index}\n{section}\n"
-            blocks.append(block)
-            length += len(block)
-    return "\n".join(blocks), BUILTIN_INPUT_SOURCE
-
-
-def _prepare_device(device: str) -> None:
-    if str(device).startswith("npu"):
-        raise RuntimeError("calibration runs on HIP devices ('cuda' in torch); 'npu' is not available")
-
-
-def _empty_device_cache(device: str, *, all_devices: bool = False) -> None:
-    if not torch.cuda.is_available():
-        return
-    current = torch.cuda.current_device()
-    indices = range(torch.cuda.device_count()) if all_devices else (current,)
-    for index in indices:
-        with torch.cuda.device(index):
-            torch.cuda.empty_cache()
-
-
-def _dtype_name(value: Any) -> str:
-    name = str(value).replace("torch.", "").lower()
-    return {"half": "float16", "float": "float32", "auto": "bfloat16"}.get(name, name)
-
-
-def _torch_dtype(value: str) -> torch.dtype:
-    choices = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
-    try:
-        return choices[_dtype_name(value)]
-    except KeyError as error:
-        raise ValueError(f"unsupported calibration dtype: {value}") from error
-
-
-def _sha256_json(value: Any) -> str:
-    text = json.dumps(value, sort_keys=True, separators=(",", ":"), default=str)
-    return hashlib.sha256(text.encode("utf-8")).hexdigest()
-
-
-def _model_source_fingerprint(model: str, revision: str | None) -> str:
-    """Identity of the model source: a local checkpoint directory by its file
-    manifest (names, sizes, modification times; weights are not re-read), any
-    other model id by id and revision.  Same format as pkg/calibration.py:530-552,
-    so artifacts validate on either side."""
-    path = Path(model).expanduser()
-    if not path.is_dir():
-        return "identifier:" + hashlib.sha256(f"{model}@{revision or 'default'}".encode()).hexdigest()
-    patterns = ("*.safetensors", "*.bin", "*.pt", "*.index.json", "config.json")
-    files = sorted({p for pattern in patterns for p in path.glob(pattern) if p.is_file()})
-    if not files:
-        raise ValueError(f"model directory contains no recognized checkpoint files: {path}")
-    entries = [(str(p.relative_to(path)), int(p.stat().st_size), int(p.stat().st_mtime_ns)) for p in files]
-    return "local-manifest:" + _sha256_json(entries)
-
-
-# --------------------------------------------------------------------- CLI --
-
-
-def _build_parser() -> argparse.ArgumentParser:
-    parser = argparse.ArgumentParser(description="Generate model-matched TriAttention calibration statistics.")
-    parser.add_argument("--model", required=True)
-    parser.add_argument("--output", required=True, type=Path)
-    parser.add_argument("--input", dest="input_path", type=Path)
-    parser.add_argument("--tokenizer")
-    parser.add_argument("--revision")
-    parser.add_argument("--tokenizer-revision")
-    parser.add_argument("--max-length", type=int, default=4096)
-    parser.add_argument("--device", default="cuda")
-    parser.add_argument(
-        "--device-map", choices=("auto",), help="Distribute a large temporary calibration model across visible devices."
-    )
-    parser.add_argument("--dtype", choices=("float16", "bfloat16", "float32"), default="bfloat16")
-    parser.add_argument("--attn-implementation", choices=("eager", "sdpa", "flash_attention_2"), default="eager")
-    parser.add_argument("--trust-remote-code", action="store_true")
-    parser.add_argument("--local-files-only", action="store_true")
-    parser.add_argument("--force", action="store_true")
-    return parser
+def build_parser() -> argparse.ArgumentParser:
+    """Command line of the generator (the reference's flags and defaults, with
+    a HIP device by default)."""
+    p = argparse.ArgumentParser(description="Generate model-matched TriAttention calibration statistics.")
+    p.add_argument("--model", required=True, help="model id or local checkpoint directory")
+    p.add_argument("--output", required=True, type=Path, help="artifact path (.pt)")
+    p.add_argument("--input", dest="input_path", type=Path, help="calibration text file (default: built-in text)")
+    p.add_argument("--tokenizer", help="tokenizer id or directory (default: the model)")
+    p.add_argument("--revision")
+    p.add_argument("--tokenizer-revision")
+    p.add_argument("--max-length", type=int, default=4096, help="calibration tokens (at least 128)")
+    p.add_argument("--device", default="cuda", help="where the temporary model runs")
+    p.add_argument("--device-map", choices=("auto",), help="spread a large temporary model over the visible devices")
+    p.add_argument("--dtype", choices=tuple(_TORCH_DTYPES), default="bfloat16")
+    p.add_argument("--attn-implementation", choices=("eager", "sdpa", "flash_attention_2"), default="eager")
+    p.add_argument("--trust-remote-code", action="store_true")
+    p.add_argument("--local-files-only", action="store_true")
+    p.add_argument("--force", action="store_true", help="regenerate even if the output exists")
+    return p
 
 
 def main(argv: Sequence[str] | None = None) -> int:
-    args = _build_parser().parse_args(argv)
-    request = CalibrationRequest(
-        model=args.model,
-        output=args.output,
-        input_path=args.input_path,
-        tokenizer=args.tokenizer,
-        revision=args.revision,
-        tokenizer_revision=args.tokenizer_revision,
-        trust_remote_code=args.trust_remote_code,
-        local_files_only=args.local_files_only,
-        max_length=args.max_length,
-        device=args.device,
-        device_map=args.device_map,
-        dtype=args.dtype,
-        attn_implementation=args.attn_implementation,
-        force=args.force,
-    )
+    args = vars(build_parser().parse_args(argv))
+    request = CalibrationRequest(**args)
     generated = generate_calibration_artifact(request)
-    print(f"{'generated' if generated else 'reused'} calibration artifact: {args.output}")
+    print(f"{'generated' if generated else 'reused'} calibration artifact: {request.output}")
     return 0
 
 
