@@ -31,7 +31,8 @@ sys.path.insert(0, str(REPO / "vllm-ascend-kvcompress-hust_amd"))
 HBM_PEAK_GBS = 8000.0
 # KV pool of the default workload as a serving deployment sizes it: most of
 # the 288 GB left after a 14B model's weights, 2 GiB per layer and K/V buffer
-# (192 GiB over 48 layers), with the batch's pages scattered through it.
+# (192 GiB over 48 layers), with the batch's pages scattered through it.  The
+# bench measures the workload's own pool first and this one second.
 SERVING_POOL_PAGES = {2: 8192}
 
 
@@ -45,10 +46,18 @@ def parse_args() -> argparse.Namespace:
     p.add_argument(
         "--pool-pages",
         type=int,
+        default=0,
+        help="pages per layer and K/V buffer of the KV pool; 0 (default) = exactly the pages the workload names "
+        "(the Qwen2.5-14B 16x16384 workload: 2048 source + 512 destination pages), larger = a bigger pool with "
+        "the workload's pages scattered through it at random",
+    )
+    p.add_argument(
+        "--serving-pool-pages",
+        type=int,
         default=None,
-        help="pages per layer and K/V buffer of the KV pool (default: 8192 = 2 GiB per buffer for the "
-        "Qwen2.5-14B 16x16384 workload, the size a serving deployment gives its pool; 0 = only the pages "
-        "the workload names); the workload's pages are scattered through the pool at random",
+        help="after the main measurement, measure the same workload again in a pool of this many pages per "
+        "buffer and report it beside the main figure (default: 8192 = 2 GiB per buffer for the Qwen2.5-14B "
+        "16x16384 workload, the size a serving deployment of a 14B model gives its KV pool; 0 = skip)",
     )
     p.add_argument(
         "--arena",
@@ -351,6 +360,44 @@ def cpu_baseline(cache, spec, repeats: int, score_aggregation: str = "mean") -> 
     }
 
 
+def step_hbm(spec, ms_per_step: float) -> dict:
+    algo = spec.algorithmic_bytes()
+    gbs = algo["total"] / (ms_per_step / 1000.0) / 1e9
+    return {"algorithmic_bytes": algo["total"], "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def measure(spec, args) -> dict:
+    """Build the workload's cache and pipeline, time exactly args.steps steps
+    (after args.warmup), then the per-stage pass; returns the figures and the
+    cache (kept alive for the CPU baseline)."""
+    import torch
+
+    from kvcompress_mi355x import workloads
+
+    device = torch.device("cuda:0")
+    cache = workloads.build_synthetic_cache(spec, device, seed=0, arena=args.arena)
+    pipeline, batch = workloads.build_pipeline(cache, score_aggregation=args.score_aggregation)
+    torch.cuda.synchronize()
+    restore = FrontRestore(cache, spec.budget) if args.restore_front else None
+    wall, timed_compact_ms = time_steps(pipeline, batch, args.steps, args.warmup, graph=args.graph, restore=restore)
+    stage_ms = stage_times(pipeline, batch, max(1, min(args.steps, 20)), restore=restore)
+    # The roofline's kernel time: events around kvc_compact inside the timed
+    # steps (graph replays have none inside: the per-stage pass then).
+    pool = cache.k_caches[0]
+    return {
+        "cache": cache,
+        "ms_per_step": 1000.0 * wall / args.steps,
+        "compact_ms": timed_compact_ms if timed_compact_ms is not None else stage_ms["compact"],
+        "compact_timing": "HIP events around kvc_compact in the timed steps"
+        if timed_compact_ms is not None
+        else "HIP events around kvc_compact in the per-stage pass",
+        "stages_ms": stage_ms,
+        "kv_pool": ("one arena, per-layer K/V views" if args.arena else "one allocation per layer and K/V")
+        + f", {pool.shape[0]} pages each ({pool.numel() * pool.element_size() / 2**30:.2f} GiB)"
+        + (", workload pages scattered through it" if spec.permute_pages else ""),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -370,49 +417,30 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     overrides = {} if args.layers is None else {"n_layers": args.layers}
-    pool_pages = args.pool_pages
-    if pool_pages is None:
-        pool_pages = SERVING_POOL_PAGES.get(args.config, 0)
-    if pool_pages:
-        overrides["pool_pages"] = pool_pages
+    if args.pool_pages:
+        overrides["pool_pages"] = args.pool_pages
     spec = workloads.config_spec(args.config, **overrides)
-    device = torch.device("cuda:0")
-    cache = workloads.build_synthetic_cache(spec, device, seed=0, arena=args.arena)
-    pipeline, batch = workloads.build_pipeline(cache, score_aggregation=args.score_aggregation)
-    torch.cuda.synchronize()
-
-    restore = None
-    if args.restore_front:
-        if not spec.inplace:
-            print("--restore-front applies to in-place workloads only", file=sys.stderr)
-            return 2
-        restore = FrontRestore(cache, spec.budget)
-    wall, timed_compact_ms = time_steps(pipeline, batch, args.steps, args.warmup, graph=args.graph, restore=restore)
-    stage_ms = stage_times(pipeline, batch, max(1, min(args.steps, 20)), restore=restore)
-    # The roofline's kernel time: events around kvc_compact inside the timed
-    # steps (graph replays have none inside: the per-stage pass then).
-    compact_ms = timed_compact_ms if timed_compact_ms is not None else stage_ms["compact"]
-    ms_per_step = 1000.0 * wall / args.steps
+    if args.restore_front and not spec.inplace:
+        print("--restore-front applies to in-place workloads only", file=sys.stderr)
+        return 2
+    m = measure(spec, args)
+    cache = m.pop("cache")
     tokens = spec.total_tokens
-    value = tokens / (wall / args.steps)
     algo = spec.algorithmic_bytes()
-    compact_gbs = algo["compact"] / (compact_ms / 1000.0) / 1e9
-    total_gbs = algo["total"] / (ms_per_step / 1000.0) / 1e9
-    score_gbs = algo["score"] / (stage_ms["score"] / 1000.0) / 1e9
-
+    compact_gbs = algo["compact"] / (m["compact_ms"] / 1000.0) / 1e9
     traffic = None
     traffic_file = REPO / "profiles" / f"compact_traffic_config{args.config}.json"
-    if traffic_file.is_file() and args.layers is None:
+    if traffic_file.is_file() and args.layers is None and not args.pool_pages:
         traffic = json.loads(traffic_file.read_text()).get("bytes_per_launch")
 
     result = {
         "metric": "KV tokens scored+compacted/sec at 1 GPU; achieved HBM GB/s as % of peak",
-        "value": round(value, 1),
+        "value": round(tokens / (m["ms_per_step"] / 1000.0), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(m["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -430,14 +458,12 @@ def main() -> int:
             "heads": f"{spec.num_attention_heads}q/{spec.num_kv_heads}kv",
             "head_dim": spec.head_dim,
             "compaction": "in-place" if spec.inplace else "private destinations",
-            "kv_pool": ("one arena, per-layer K/V views" if args.arena else "one allocation per layer and K/V")
-            + f", {cache.k_caches[0].shape[0]} pages each ({cache.k_caches[0].numel() * cache.k_caches[0].element_size() / 2**30:.2f} GiB)"
-            + (", workload pages scattered through it" if spec.permute_pages else ""),
+            "kv_pool": m["kv_pool"],
             "launch": "one HIP graph per step" if args.graph else "kernel launches per step",
             **({"score_aggregation": "max"} if args.score_aggregation == "max" else {}),
             **(
                 {"timing": "sum of per-step HIP-event times; overwritten front pages restored before each step, untimed"}
-                if restore is not None
+                if args.restore_front
                 else {}
             ),
         },
@@ -450,21 +476,34 @@ def main() -> int:
             "frac": round(compact_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "algorithmic_bytes": algo["compact"],
-            "kernel_ms": round(compact_ms, 4),
-            "timing": "HIP events around kvc_compact in the timed steps"
-            if timed_compact_ms is not None
-            else "HIP events around kvc_compact in the per-stage pass",
+            "kernel_ms": round(m["compact_ms"], 4),
+            "timing": m["compact_timing"],
         },
-        "step_hbm": {
-            "algorithmic_bytes": algo["total"],
-            "achieved_gbs": round(total_gbs, 1),
-            "frac": round(total_gbs / HBM_PEAK_GBS, 4),
-        },
-        "stages_ms": {k: round(v, 4) for k, v in stage_ms.items()},
-        "score_gbs": round(score_gbs, 1),
+        "step_hbm": step_hbm(spec, m["ms_per_step"]),
+        "stages_ms": {k: round(v, 4) for k, v in m["stages_ms"].items()},
+        "score_gbs": round(algo["score"] / (m["stages_ms"]["score"] / 1000.0) / 1e9, 1),
     }
+    serving = args.serving_pool_pages
+    if serving is None:
+        serving = SERVING_POOL_PAGES.get(args.config, 0) if args.layers is None and not args.pool_pages else 0
+    if serving:
+        # The same workload in a serving-sized pool, measured after the main
+        # figure in a fresh allocation (the main cache is released first).
+        del cache
+        torch.cuda.empty_cache()
+        sspec = workloads.config_spec(args.config, **{**overrides, "pool_pages": serving})
+        sm = measure(sspec, args)
+        cache = sm.pop("cache")
+        result["serving_pool"] = {
+            "kv_pool": sm["kv_pool"],
+            "value": round(tokens / (sm["ms_per_step"] / 1000.0), 1),
+            "ms_per_step": round(sm["ms_per_step"], 4),
+            "step_hbm_frac": step_hbm(sspec, sm["ms_per_step"])["frac"],
+            "compact_ms": round(sm["compact_ms"], 4),
+            "compact_frac": round(algo["compact"] / (sm["compact_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+        }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cache, spec, args.cpu_repeats, args.score_aggregation)
+        result["cpu_baseline"] = cpu_baseline(cache, cache.spec, args.cpu_repeats, args.score_aggregation)
     print(json.dumps(result), flush=True)
     return 0
 

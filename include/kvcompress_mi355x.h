@@ -280,13 +280,23 @@ int kvc_select_keep_split(kvc_stream_t stream, int n_seq, int max_seq_len, const
  * are the front pages of the source table (dst page i/128 = source page i/128);
  * the kernel orders every read of a row before the write that overwrites it.
  * Otherwise destination pages must be private (disjoint from the source pages).
- * row_elems = kv_heads*head_dim; elem_bytes = 2. */
+ * row_elems = kv_heads*head_dim; elem_bytes = 2.
+ * workspace: NULL, or at least kvc_compact_workspace_bytes(n_seq, budget)
+ * bytes, 16-byte aligned, any contents.  With it, private-destination batches
+ * of at most 32 sequences first resolve every kept row's source and
+ * destination offsets into it and then move the rows one layer per workgroup
+ * (a small address-translation working set: the same time whatever the
+ * physical placement of the pool); without it, or for larger batches and in
+ * place, a workgroup resolves its rows once and walks every layer.  Both give
+ * identical caches. */
+size_t kvc_compact_workspace_bytes(int n_seq, int budget);
 int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_layer_ptrs,
                 const uint64_t* v_layer_ptrs, int64_t num_pages, int64_t page_stride,
                 int64_t row_elems, int elem_bytes, int n_seq, const int32_t* seq_lens,
                 const int64_t* src_block_offsets, const int64_t* src_block_ids,
                 const int64_t* dst_block_offsets, const int64_t* dst_block_ids,
-                const int64_t* keep, int64_t keep_stride, int budget);
+                const int64_t* keep, int64_t keep_stride, int budget, void* workspace,
+                size_t workspace_bytes);
 
 /* New block table and released pages after compaction (PendingCompression and
  * the scheduler commit, pkg/provider.py:596-601, pkg/stateful.py:327-338):

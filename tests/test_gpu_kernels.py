@@ -606,9 +606,13 @@ def _layers(g, n_layers, pages, kv, dim, dtype):
     return ks, vs
 
 
+@pytest.mark.parametrize("path", ["walk", "plan"])
 @pytest.mark.parametrize("mode", ["private", "inplace"])
 @pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided", "split"])
-def test_compact_bit_exact(hip_device, mode: str, pattern: str) -> None:
+def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> None:
+    """Both private-mode forms (rows resolved per workgroup and every layer
+    walked, or rows planned once into the workspace and moved one layer per
+    workgroup) and the in-place walk, against the reference materialisation."""
     _, _, cache = _kvc()
     from kvcompress_mi355x.methods.triattention import _device as dev
 
@@ -671,6 +675,9 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str) -> None:
         dst_block_ids=di,
         keep=keep,
         budget=budget,
+        workspace=None
+        if path == "walk"
+        else torch.full((cache.compact_workspace_bytes(len(lens), budget),), 0xAB, dtype=torch.uint8, device=hip_device),
     )
     torch.cuda.synchronize()
     for layer in range(n_layers):
@@ -683,6 +690,71 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str) -> None:
         want_table, want_freed = ref.rewrite_block_table(src_tables[b], dst_tables[b] if mode == "private" else None, budget)
         assert tables[b].cpu().tolist() == want_table
         assert freed[b].cpu().tolist() == want_freed
+
+
+@pytest.mark.parametrize("kv,dim", [(1, 128), (4, 128), (8, 128), (10, 128)], ids=["256B", "1KB", "2KB", "2560B"])
+def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
+    """The planned private form for row widths that give 1, 2 or 8 rows per
+    128-thread workgroup and rows split into two column slices (2560 B), with
+    an unmapped destination page, bit-exact against the walked form and the
+    reference materialisation."""
+    _, _, cache = _kvc()
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    g = torch.Generator().manual_seed(kv * 100 + dim)
+    n_layers, budget = 2, 384
+    lens = [1000, 700, 385, 900]
+    pool = sum(-(-n // 128) for n in lens) + 3 * len(lens) + 2
+    perm = torch.randperm(pool, generator=g).tolist()
+    cur, src_tables, dst_tables = 0, [], []
+    for n in lens:
+        src_tables.append(perm[cur : cur + -(-n // 128)])
+        cur += -(-n // 128)
+    for _ in lens:
+        dst_tables.append(perm[cur : cur + 3])
+        cur += 3
+    dst_tables[2][1] = -1  # an unmapped destination page: its rows move nowhere
+    keeps = [torch.sort(torch.randperm(n, generator=g)[:budget]).values for n in lens]
+    ks, vs = _layers(g, n_layers, pool, kv, dim, torch.bfloat16)
+    results = {}
+    for path in ("walk", "plan"):
+        ks_d = [k.to(hip_device) for k in ks]
+        vs_d = [v.to(hip_device) for v in vs]
+        so, si, _ = dev.ragged(src_tables, hip_device)
+        do, di, _ = dev.ragged(dst_tables, hip_device)
+        cache.compact_layers(
+            dev.pointer_table(ks_d, hip_device),
+            dev.pointer_table(vs_d, hip_device),
+            num_pages=pool,
+            page_stride=int(ks_d[0].stride(0)),
+            row_elems=kv * dim,
+            seq_lens=torch.tensor(lens, dtype=torch.int32, device=hip_device),
+            src_block_offsets=so,
+            src_block_ids=si,
+            dst_block_offsets=do,
+            dst_block_ids=di,
+            keep=torch.stack(keeps).to(hip_device),
+            budget=budget,
+            workspace=None
+            if path == "walk"
+            else torch.empty(cache.compact_workspace_bytes(len(lens), budget), dtype=torch.uint8, device=hip_device),
+        )
+        torch.cuda.synchronize()
+        results[path] = ([k.cpu() for k in ks_d], [v.cpu() for v in vs_d])
+    for b in range(len(lens)):
+        dst = [p for p in dst_tables[b]]
+        rows = [i for i in range(budget) if dst[i // 128] >= 0]
+        keep_b = keeps[b][rows]
+        for layer in range(n_layers):
+            for kind, src_cache in ((0, ks), (1, vs)):
+                want = ref.gather_paged_tokens(src_cache[layer], torch.tensor(src_tables[b]), keep_b, 128)
+                for path in ("walk", "plan"):
+                    got_cache = results[path][kind][layer].view(-1, kv, dim)
+                    slots = torch.tensor([dst[i // 128] * 128 + i % 128 for i in rows])
+                    assert torch.equal(got_cache[slots], want), (path, b, layer, kind)
+    for kind in range(2):
+        for layer in range(n_layers):
+            assert torch.equal(results["walk"][kind][layer], results["plan"][kind][layer])
 
 
 def test_materialize_token_slots_padded_pages(hip_device) -> None:

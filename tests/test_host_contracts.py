@@ -287,7 +287,7 @@ def test_workspace_query_and_argument_validation_without_gpu() -> None:
     with pytest.raises(ValueError, match="budget"):
         _native.call("kvc_select_keep", None, 1, 10, None, None, None, 20, 0, 0, 1, 0, None, 20)
     with pytest.raises(ValueError):
-        _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4)
+        _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4, None, 0)
 
 
 def test_max_scorer_queries_and_validation_without_gpu() -> None:

@@ -37,32 +37,50 @@ namespace {
 
 // ------------------------------------------------------------- phase tables --
 
-// One thread per (sequence, layer, frequency).  The phase argument is formed
-// exactly as the torch path does in float32, (offset + round_start) * omega,
-// and its cosine/sine are evaluated in double and rounded once, so the table
-// agrees with a correctly rounded float32 evaluation.  The mean is a
-// sequential float32 sum in offset order divided by the offset count.
-__global__ void mean_phases_kernel(int n_seq, int n_layers, int n_freq,
-                                   const int64_t* __restrict__ round_starts,
-                                   const float* __restrict__ offsets, int n_offsets,
-                                   const float* __restrict__ omega, float* __restrict__ phase_cos,
-                                   float* __restrict__ phase_sin) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+// One group of `width` lanes (the offset count rounded up to a power of two,
+// at most 32) per (sequence, layer, frequency); lane o evaluates offset o (then
+// o + width, ...), so a thread waits for one cosine/sine instead of one per
+// offset.  The phase argument is formed exactly as the torch path does in
+// float32, (offset + round_start) * omega, and its cosine/sine are evaluated in
+// double and rounded once, so the table agrees with a correctly rounded float32
+// evaluation.  Lane 0 of the group sums the rounded values sequentially in
+// offset order in float32 and divides by the offset count, as the torch path's
+// mean over the offset axis.
+constexpr int kPhaseMaxLanes = 32;
+
+__global__ __launch_bounds__(256) void mean_phases_kernel(int n_seq, int n_layers, int n_freq, int width,
+                                                          const int64_t* __restrict__ round_starts,
+                                                          const float* __restrict__ offsets, int n_offsets,
+                                                          const float* __restrict__ omega, float* __restrict__ phase_cos,
+                                                          float* __restrict__ phase_sin) {
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / width;
+  const int lane = threadIdx.x & (width - 1);
   const int64_t per_seq = static_cast<int64_t>(n_layers) * n_freq;
-  if (idx >= per_seq * n_seq) return;
+  if (idx >= per_seq * n_seq) return;  // the whole lane group leaves together
   const int64_t b = idx / per_seq;
   const int64_t lf = idx - b * per_seq;
   const float rs = static_cast<float>(round_starts[b]);
   const float w = omega[lf];
   float c = 0.0f, s = 0.0f;
-  for (int o = 0; o < n_offsets; ++o) {
-    const float x = __fmul_rn(__fadd_rn(offsets[o], rs), w);
-    c = __fadd_rn(c, static_cast<float>(cos(static_cast<double>(x))));
-    s = __fadd_rn(s, static_cast<float>(sin(static_cast<double>(x))));
+  for (int o0 = 0; o0 < n_offsets; o0 += width) {
+    const int o = o0 + lane;
+    float co = 0.0f, so = 0.0f;
+    if (o < n_offsets) {
+      const float x = __fmul_rn(__fadd_rn(offsets[o], rs), w);
+      co = static_cast<float>(cos(static_cast<double>(x)));
+      so = static_cast<float>(sin(static_cast<double>(x)));
+    }
+    const int count = min(width, n_offsets - o0);
+    for (int j = 0; j < count; ++j) {
+      c = __fadd_rn(c, __shfl(co, j, width));
+      s = __fadd_rn(s, __shfl(so, j, width));
+    }
   }
-  const float n = static_cast<float>(n_offsets);
-  phase_cos[idx] = __fdiv_rn(c, n);
-  phase_sin[idx] = __fdiv_rn(s, n);
+  if (lane == 0) {
+    const float n = static_cast<float>(n_offsets);
+    phase_cos[idx] = __fdiv_rn(c, n);
+    phase_sin[idx] = __fdiv_rn(s, n);
+  }
 }
 
 // One thread per (sequence, layer, offset, frequency): cos and sin of the
@@ -615,8 +633,11 @@ extern "C" int kvc_mean_phases(kvc_stream_t stream, int n_seq, int n_layers, int
   if (!round_starts || !offsets || !omega || !phase_cos || !phase_sin)
     return fail(KVC_EINVAL, "kvc_mean_phases: null pointer");
   const int64_t total = static_cast<int64_t>(n_seq) * n_layers * n_freq;
-  mean_phases_kernel<<<static_cast<unsigned>(ceil_div(total, 256)), 256, 0, as_stream(stream)>>>(
-      n_seq, n_layers, n_freq, round_starts, offsets, n_offsets, omega, phase_cos, phase_sin);
+  int width = 1;
+  while (width < n_offsets && width < kPhaseMaxLanes) width <<= 1;
+  if (ceil_div(total * width, 256) > 0x7fffffff) return fail(KVC_EINVAL, "kvc_mean_phases: grid too large");
+  mean_phases_kernel<<<static_cast<unsigned>(ceil_div(total * width, 256)), 256, 0, as_stream(stream)>>>(
+      n_seq, n_layers, n_freq, width, round_starts, offsets, n_offsets, omega, phase_cos, phase_sin);
   return launch_status("kvc_mean_phases");
 }
 

@@ -81,9 +81,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_select_keep": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i64]),
     "kvc_select_workspace_bytes": (_sz, [_i32, _i32, _i32]),
     "kvc_select_keep_split": (_i32, [_p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _sz]),
+    "kvc_compact_workspace_bytes": (_sz, [_i32, _i32]),
     "kvc_compact": (
         _i32,
-        [_p, _i32, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32],
+        [_p, _i32, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _sz],
     ),
     "kvc_rewrite_block_tables": (_i32, [_p, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]),
     "kvc_token_slots": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p]),

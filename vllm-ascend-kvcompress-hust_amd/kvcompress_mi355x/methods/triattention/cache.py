@@ -138,8 +138,14 @@ def compact_layers(
     dst_block_ids: torch.Tensor | None,
     keep: torch.Tensor,
     budget: int,
+    workspace: torch.Tensor | None = None,
 ) -> None:
-    """Move every layer's kept K/V rows in one launch (``dst_block_ids`` None = in place)."""
+    """Move every layer's kept K/V rows (``dst_block_ids`` None = in place).
+
+    ``workspace`` (uint8, at least :func:`compact_workspace_bytes`) lets a
+    private-destination batch of up to 32 sequences resolve its rows once and
+    move them one layer per workgroup; without it every workgroup walks all
+    layers.  The caches end up identical either way."""
     n_layers = int(k_layer_ptrs.numel())
     if int(v_layer_ptrs.numel()) != n_layers:
         raise ValueError("K and V layer tables differ in length")
@@ -163,7 +169,14 @@ def compact_layers(
         dev.ptr(keep),
         int(keep.stride(0)),
         int(budget),
+        dev.ptr(workspace),
+        0 if workspace is None else int(workspace.numel() * workspace.element_size()),
     )
+
+
+def compact_workspace_bytes(n_seq: int, budget: int) -> int:
+    """Bytes of the optional :func:`compact_layers` workspace for a batch."""
+    return int(_native.load().kvc_compact_workspace_bytes(int(n_seq), int(budget)))
 
 
 def rewrite_block_tables(

@@ -33,7 +33,7 @@ import torch
 
 from ... import _native
 from . import _device as dev
-from .cache import compact_layers, rewrite_block_tables
+from .cache import compact_layers, compact_workspace_bytes, rewrite_block_tables
 from .selection import POLICY_CODES, prefers_split, select_keep_indices_batched, select_workspace, validate_selection
 
 
@@ -261,6 +261,7 @@ class CompressionPipeline:
         self.agg = torch.empty(self.max_tokens, dtype=torch.float32, device=dev_)
         self.keep = torch.empty((self.max_seqs, self.budget), dtype=torch.int64, device=dev_)
         self.select_ws = select_workspace(self.max_seqs, self.segments, self.policy, dev_)
+        self.compact_ws = torch.empty(compact_workspace_bytes(self.max_seqs, self.budget), dtype=torch.uint8, device=dev_)
         self.layer_scores = None  # flat per-layer head maxima, viewed [S, tokens]; made on first use
         shape = (s, self.kv_heads, self.head_dim, self.tables.rotary_dim, self.tables.qpk, self.max_seqs, self.max_seq_len)
         if self.score_aggregation == "max":
@@ -529,6 +530,7 @@ class CompressionPipeline:
             dst_block_ids=batch.dst_ids,
             keep=self.keep,
             budget=self.budget,
+            workspace=self.compact_ws,
         )
 
     def rewrite(self, batch: Batch) -> tuple[torch.Tensor, list[torch.Tensor]]:
