@@ -53,40 +53,19 @@ namespace {
 // 1.50 ms (4 x 4608 rows kept of 131072, in place), 0.286 vs 0.296 ms
 // (Qwen3.5 shape, 1 KB rows); 2 or 4 rows per thread and 1024 threads were
 // slower on all three, 128 threads level with 256.
-#ifndef KVC_COPY_UNROLL
-#define KVC_COPY_UNROLL 1
-#endif
-#ifndef KVC_COPY_THREADS
-#define KVC_COPY_THREADS 256
-#endif
 // In-place mode walks its tiles in order behind a barrier; 2 rows per thread
 // at 512 threads measured 0.85 ms on the 4 x 131072-token shape (48 layers,
 // 4608 kept rows) against 1.32 ms for 8 rows at 256 threads.
-#ifndef KVC_INPLACE_UNROLL
-#define KVC_INPLACE_UNROLL 2
-#endif
-#ifndef KVC_INPLACE_THREADS
-#define KVC_INPLACE_THREADS 512
-#endif
-#ifndef KVC_COPY_NT_LOAD
-#define KVC_COPY_NT_LOAD 1
-#endif
-#ifndef KVC_COPY_NT_STORE
-#define KVC_COPY_NT_STORE 1
-#endif
-#ifndef KVC_COPY_MAX_WORD
-#define KVC_COPY_MAX_WORD 16
-#endif
 
-constexpr int kCopyThreads = KVC_COPY_THREADS;
+constexpr int kCopyThreads = 256;
 // Planned private mode: 128-thread workgroups (one 2 KB row per workgroup; 128
 // and 256 threads measured level, 512 and 1024 slower) for batches of at most
 // kPlanMaxSeqs sequences.
 constexpr int kPlanThreads = 128;
 constexpr int kPlanMaxSeqs = 32;
-constexpr int kCopyUnroll = KVC_COPY_UNROLL;  // rows per thread per tile (private mode)
-constexpr int kInplaceThreads = KVC_INPLACE_THREADS;
-constexpr int kInplaceUnroll = KVC_INPLACE_UNROLL;  // rows per thread per tile (in place)
+constexpr int kCopyUnroll = 1;  // rows per thread per tile (private mode)
+constexpr int kInplaceThreads = 512;
+constexpr int kInplaceUnroll = 2;  // rows per thread per tile (in place)
 
 // Native vector words (the HIP_vector_type structs would be kept in scratch).
 typedef uint32_t w128 __attribute__((ext_vector_type(4)));
@@ -121,15 +100,11 @@ constexpr int kRowsSafe = 2;    // keep[i] >= budget (in place, any order)
 // Streaming word access; the non-temporal forms mark lines for early eviction.
 template <typename Chunk>
 __device__ __forceinline__ Chunk load_word(KVC_GLOBAL const char* p) {
-  if (KVC_COPY_NT_LOAD) return __builtin_nontemporal_load(reinterpret_cast<KVC_GLOBAL const Chunk*>(p));
-  return *reinterpret_cast<KVC_GLOBAL const Chunk*>(p);
+  return __builtin_nontemporal_load(reinterpret_cast<KVC_GLOBAL const Chunk*>(p));
 }
 template <typename Chunk>
 __device__ __forceinline__ void store_word(KVC_GLOBAL char* p, Chunk v) {
-  if (KVC_COPY_NT_STORE)
-    __builtin_nontemporal_store(v, reinterpret_cast<KVC_GLOBAL Chunk*>(p));
-  else
-    *reinterpret_cast<KVC_GLOBAL Chunk*>(p) = v;
+  __builtin_nontemporal_store(v, reinterpret_cast<KVC_GLOBAL Chunk*>(p));
 }
 
 __device__ __forceinline__ int64_t page_of(const int64_t* table, int64_t n_entries, int64_t row,
@@ -467,7 +442,7 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
   ca.keep_stride = keep_stride;
 
   // Widest word that divides both the row and the page stride.
-  int word = KVC_COPY_MAX_WORD;
+  int word = 16;
   while (word > 2 && ((ca.row_bytes % word) != 0 || (ca.page_stride_bytes % word) != 0)) word >>= 1;
   ca.row_chunks = ca.row_bytes / word;
 

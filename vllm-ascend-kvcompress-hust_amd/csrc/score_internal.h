@@ -5,10 +5,7 @@
 
 namespace kvc {
 
-#ifndef KVC_SCORE_TILE
-#define KVC_SCORE_TILE 256
-#endif
-constexpr int kScoreTile = KVC_SCORE_TILE;  // tokens per scoring workgroup
+constexpr int kScoreTile = 256;  // tokens per scoring workgroup
 constexpr int kScoreThreads = 256;  // 4 waves
 constexpr int kUnroll = 4;          // token iterations with loads in flight
 static_assert(kScoreTile % kBlockSize == 0, "a scoring span starts and ends on page boundaries");

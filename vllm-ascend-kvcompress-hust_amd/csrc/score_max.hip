@@ -19,7 +19,7 @@
 // in the reference.
 //
 // Work split: a workgroup owns one KV head, a group of its query heads (all of
-// them when their fragments fit the LDS budget) and KVC_MAX_SPANS consecutive
+// them when their fragments fit the LDS budget) and kMaxSpans consecutive
 // 256-token spans; its four waves walk interleaved 16-token tiles of a span.
 // The per-offset fragments (bf16 or fp16 hi/lo, 1 KB per 32 rotary dims and
 // chunk) are staged in LDS once per workgroup; each fragment read feeds two
@@ -34,18 +34,12 @@
 
 #include "mfma_common.h"
 
-#ifndef KVC_MAX_FRAG_LDS
-#define KVC_MAX_FRAG_LDS (48 * 1024)  // bytes of per-offset fragments staged per workgroup
-#endif
-#ifndef KVC_MAX_SPANS
-#define KVC_MAX_SPANS 4  // 256-token spans per workgroup
-#endif
 
 namespace kvc {
 namespace {
 
-constexpr int kMaxSpans = KVC_MAX_SPANS;
-constexpr int kMaxFragLds = KVC_MAX_FRAG_LDS;
+constexpr int kMaxSpans = 4;  // 256-token spans per workgroup
+constexpr int kMaxFragLds = 48 * 1024;  // bytes of per-offset fragments staged per workgroup
 constexpr int kOffsetFragBytes = 64 * 16;  // one B operand: 64 lanes x 8 16-bit values
 
 struct OffsetFoldArgs {

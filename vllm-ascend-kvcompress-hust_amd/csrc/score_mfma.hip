@@ -42,9 +42,6 @@
 
 #include "mfma_common.h"
 
-#ifndef KVC_MFMA_GROUP
-#define KVC_MFMA_GROUP 2  // 16-token tiles per prefetch group
-#endif
 
 namespace kvc {
 namespace {
@@ -339,9 +336,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_mfma_kernel(ScoreArgs a, 
     }
   };
 
-  // Tiles sub, sub + nsub, ... in groups of KVC_MFMA_GROUP; the next group's
+  // Tiles sub, sub + nsub, ... in groups of G; the next group's
   // keys are in flight while the current group is scored.
-  constexpr int G = KVC_MFMA_GROUP;
+  constexpr int G = 2;  // 16-token tiles per prefetch group
   u32x4 ka[G][NK], kb2[G][NK];
   const int step = geo.nsub;
   int mt = sub;

@@ -37,18 +37,9 @@ constexpr int kSelThreads = 1024;   // one workgroup per job
 constexpr int kSplitThreads = 256;  // split path: one workgroup per chunk
 constexpr int kSplitChunk = 4096;   // keys per chunk, at least
 constexpr int kSplitMaxChunks = 64;
-#ifndef KVC_SEL_UNROLL
-#define KVC_SEL_UNROLL 4
-#endif
-#ifndef KVC_EMIT_WORDS
-#define KVC_EMIT_WORDS 2
-#endif
-#ifndef KVC_SEL_PEEL
-#define KVC_SEL_PEEL 1
-#endif
-constexpr int kSelUnroll = KVC_SEL_UNROLL;  // float4 words per thread in flight in a histogram pass
-constexpr int kEmitWords = KVC_EMIT_WORDS;  // float4 words per thread per emission tile
-constexpr int kSelPeel = KVC_SEL_PEEL;      // dominant digits counted with one atomic per wave
+constexpr int kSelUnroll = 4;  // float4 words per thread in flight in a histogram pass
+constexpr int kEmitWords = 2;  // float4 words per thread per emission tile
+constexpr int kSelPeel = 1;    // dominant digits counted with one atomic per wave
 static_assert(kSelThreads * kEmitWords * 4 < 65536, "packed emission counts need 16 bits per half");
 
 struct SelectArgs {
