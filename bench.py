@@ -96,7 +96,139 @@ def parse_args() -> argparse.Namespace:
         help="only measure calibration statistics (kvc_qstats_accumulate) over a Qwen2.5-14B-shaped calibration "
         "pass: 48 layers of 4096-token bf16 query projections (40 heads x 128), one buffer per layer",
     )
+    p.add_argument(
+        "--tp-rank-scorer",
+        action="store_true",
+        help="only measure the one-layer scorer on one tensor-parallel rank's share of a Qwen3.5-35B-A3B cache: "
+        "1 KV head, 8 query heads, head_dim 256 with 64 rotary dims, 32768 bf16 tokens in contiguous 128-token "
+        "pages, 16 offsets at round start 65536 (the shape of the reference's partial-RoPE scorer benchmark, "
+        "tests/run_npu_partial_rope_benchmark.py)",
+    )
     return p.parse_args()
+
+
+def tp_rank_scorer_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -> int:
+    """kvc_score_paged (through the reference-named wrapper
+    score_paged_keys_mean_precomputed) on one rank's share of a Qwen3.5 cache:
+    inputs drawn as the reference's benchmark draws them
+    (tests/run_npu_partial_rope_benchmark.py:35-96).  Algorithmic bytes = the
+    keys read once, 32768 x 256 x 2 B = 16.8 MB per call."""
+    import torch
+
+    from kvcompress_mi355x.methods.triattention import kernels
+
+    device = torch.device("cuda:0")
+    tokens, block, rotary, head_dim, kv_heads, qpk = 32768, 128, 64, 256, 1, 8
+    freq = rotary // 2
+    round_start = 65536
+    g = torch.Generator(device=device).manual_seed(20260927)
+    cache = torch.randn(tokens // block, block, kv_heads, head_dim, generator=g, device=device).to(torch.bfloat16)
+    blocks = torch.arange(tokens // block, dtype=torch.int64, device=device)
+    shape = (kv_heads, qpk, freq)
+    q_real = torch.randn(shape, generator=g, device=device)
+    q_imag = torch.randn(shape, generator=g, device=device)
+    q_abs = torch.sqrt(q_real.square() + q_imag.square()) + 0.1
+    q_pass = torch.randn(kv_heads, qpk, head_dim - rotary, generator=g, device=device)
+    scale = torch.ones(shape, device=device)
+    omega = torch.logspace(0, -4, freq, device=device)
+    offsets = torch.arange(1, 17, dtype=torch.float32, device=device)
+    phase = (offsets[:, None] + round_start) * omega[None, :]
+    phase_cos = torch.cos(phase).mean(dim=0)
+    phase_sin = torch.sin(phase).mean(dim=0)
+    extra = q_abs - torch.sqrt(q_real.square() + q_imag.square() + 1e-8)
+    out = torch.empty(kv_heads, qpk, tokens, dtype=torch.float32, device=device)
+
+    def call() -> None:
+        kernels.score_paged_keys_mean_precomputed(
+            cache, blocks, q_real, q_imag, scale, extra, phase_cos, phase_sin, tokens, out, block, "half",
+            q_pass_mean=q_pass, rotary_dim=rotary,
+        )
+
+    for _ in range(max(1, warmup)):
+        call()
+    torch.cuda.synchronize()
+    # Device time per call: HIP events on the stream the wrapper launches on
+    # (the current stream), around `steps` calls.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        call()
+    end.record()
+    torch.cuda.synchronize()
+    device_ms = start.elapsed_time(end) / steps
+    # Wall time per call, as the reference's benchmark times its fused kernel.
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    torch.cuda.synchronize()
+    wall_ms = 1000.0 * (time.perf_counter() - t0) / steps
+    nbytes = tokens * kv_heads * head_dim * 2
+    result = {
+        "metric": "one-layer scorer, tokens scored/s on one tensor-parallel rank's Qwen3.5 cache share; HBM GB/s",
+        "value": round(tokens / (device_ms / 1000.0), 1),
+        "unit": "tokens/s",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(device_ms, 5),
+        "wall_ms_per_call": round(wall_ms, 5),
+        "higher_is_better": True,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3.5-35b-a3b-tp-rank-scorer-32768",
+            "tokens": tokens, "kv_heads": kv_heads, "query_heads": kv_heads * qpk, "head_dim": head_dim,
+            "rotary_dim": rotary, "offsets": 16, "round_start": round_start, "layers": 1,
+        },
+        "roofline": {
+            "kernel": "kvc_score_paged (weight fold + scorer launches)",
+            "bound": "hbm",
+            "achieved": round(nbytes / (device_ms / 1000.0) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(nbytes / (device_ms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": nbytes,
+            "timing": "HIP events around the wrapper calls on the current stream",
+        },
+    }
+    if not no_cpu:
+        from oracle import triattention_ref as ref
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        stats = ref.LayerStats(
+            q_mean_real=q_real.cpu(), q_mean_imag=q_imag.cpu(), q_abs_mean=q_abs.cpu(),
+            freq_scale_sq=scale.square().cpu(), omega=omega.cpu(), rope_style="half", rotary_dim=rotary,
+            q_pass_mean=q_pass.cpu(),
+        )
+        host_cache, host_blocks, host_offsets = cache.cpu(), blocks.cpu(), offsets.cpu()
+        reference = torch.empty(kv_heads, qpk, tokens, dtype=torch.float32)
+
+        def generic() -> float:
+            t = time.perf_counter()
+            for s0 in range(0, tokens, 8192):
+                count = min(8192, tokens - s0)
+                keys = ref.gather_paged_range(host_cache, host_blocks, start=s0, count=count, block_size=block)
+                reference[..., s0 : s0 + count] = ref.score_post_rope_keys(
+                    keys, stats, round_start=round_start, offsets=host_offsets, aggregation="mean"
+                )
+            return time.perf_counter() - t
+
+        generic()
+        med = statistics.median(generic() for _ in range(cpu_repeats))
+        hip = out.cpu()
+        err = ((hip - reference).abs() / (reference.abs() + reference.square().mean(dim=-1, keepdim=True).sqrt())).max()
+        result["cpu_baseline"] = {
+            "value": round(tokens / med, 1),
+            "unit": "tokens/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"the whole call: the torch restatement of score_post_rope_keys over 8192-token gathered chunks "
+            f"(the reference benchmark's fallback path); median of {cpu_repeats} after 1 warm-up; "
+            f"max |err| / (|ref| + rms) of the HIP scores against it {float(err):.2e}; host CPU {cpu_model()}",
+        }
+        result["speedup_vs_cpu_baseline"] = round(med * 1000.0 / device_ms, 1)
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 def calibration_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -> int:
@@ -413,6 +545,8 @@ def main() -> int:
 
     if args.calibration:
         return calibration_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
+    if args.tp_rank_scorer:
+        return tp_rank_scorer_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1

@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from ... import _native
@@ -84,3 +86,21 @@ def ragged(rows: list[torch.Tensor | list[int] | tuple[int, ...]], device: torch
         offsets.append(offsets[-1] + n)
     flat = torch.cat(parts) if parts else torch.empty(0, dtype=torch.int64, device=device)
     return torch.tensor(offsets, dtype=torch.int64, device=device), flat.contiguous(), lengths
+
+
+@functools.lru_cache(maxsize=256)
+def _one_sequence_descriptor(device_index: int, layer_ptr: int, num_tokens: int, n_blocks: int) -> torch.Tensor:
+    signed = layer_ptr - (1 << 64) if layer_ptr >= (1 << 63) else layer_ptr
+    # int64 words: [layer pointer, token offsets (0, n), block offsets (0, blocks), sequence length in the low half]
+    return torch.tensor([signed, 0, num_tokens, 0, n_blocks, num_tokens], dtype=torch.int64,
+                        device=torch.device("cuda", device_index))
+
+
+def one_sequence_descriptor(layer: torch.Tensor, num_tokens: int, n_blocks: int) -> dict[str, int]:
+    """Device addresses of the batch descriptor of a one-layer, one-sequence
+    launch (layer pointer table, token and block offsets, int32 sequence
+    length), kept on the device per distinct value so that repeated calls
+    copy nothing to the device.  The words are immutable once made."""
+    t = _one_sequence_descriptor(layer.device.index, int(layer.data_ptr()), int(num_tokens), int(n_blocks))
+    base = int(t.data_ptr())
+    return {"layer_ptrs": base, "token_offsets": base + 8, "block_offsets": base + 24, "seq_lens": base + 40}

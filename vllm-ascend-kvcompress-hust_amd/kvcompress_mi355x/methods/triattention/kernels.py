@@ -151,10 +151,7 @@ def _single_layer_scoring(
         head_dim=head_dim,
         num_tokens=num_tokens,
         blocks=blocks,
-        layer_ptrs=dev.pointer_table([k_cache], device),
-        seq_lens=torch.tensor([num_tokens], dtype=torch.int32, device=device),
-        token_offsets=torch.tensor([0, num_tokens], dtype=torch.int64, device=device),
-        block_offsets=torch.tensor([0, blocks.numel()], dtype=torch.int64, device=device),
+        desc=dev.one_sequence_descriptor(k_cache, num_tokens, blocks.numel()),
         calib=(f32(q_real), f32(q_imag), f32(frequency_scale), f32(extra_coefficient)),
         q_pass=f32(q_pass_mean) if q_pass_mean is not None else None,
     )
@@ -170,7 +167,7 @@ def _launch_single_layer(entry: str, a: dict, k_cache, rope_style, phase_args: t
         dev.stream_handle(a["device"]),
         dev.cache_dtype_code(k_cache.dtype),
         1,
-        dev.ptr(a["layer_ptrs"]),
+        a["desc"]["layer_ptrs"],
         int(k_cache.shape[0]),
         int(k_cache.stride(0)),
         a["kv_heads"],
@@ -180,9 +177,9 @@ def _launch_single_layer(entry: str, a: dict, k_cache, rope_style, phase_args: t
         dev.rope_style_code(rope_style),
         1,
         a["num_tokens"],
-        dev.ptr(a["seq_lens"]),
-        dev.ptr(a["token_offsets"]),
-        dev.ptr(a["block_offsets"]),
+        a["desc"]["seq_lens"],
+        a["desc"]["token_offsets"],
+        a["desc"]["block_offsets"],
         dev.ptr(a["blocks"]),
         dev.ptr(qr),
         dev.ptr(qi),
