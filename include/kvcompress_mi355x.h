@@ -282,13 +282,13 @@ int kvc_select_keep_split(kvc_stream_t stream, int n_seq, int max_seq_len, const
  * Otherwise destination pages must be private (disjoint from the source pages).
  * row_elems = kv_heads*head_dim; elem_bytes = 2.
  * workspace: NULL, or at least kvc_compact_workspace_bytes(n_seq, budget)
- * bytes, 16-byte aligned, any contents.  With it, private-destination batches
- * of at most 32 sequences first resolve every kept row's source and
- * destination offsets into it and then move the rows one layer per workgroup
- * (a small address-translation working set: the same time whatever the
- * physical placement of the pool); without it, or for larger batches and in
- * place, a workgroup resolves its rows once and walks every layer.  Both give
- * identical caches. */
+ * bytes, 16-byte aligned, any contents.  With it, batches of at most 32
+ * sequences first resolve every kept row's source and destination offsets
+ * into it and then move the rows one layer per workgroup (a small
+ * address-translation working set: the same time whatever the physical
+ * placement of the pool); in place, this covers the rows that follow the
+ * ordered walk.  Without it, or for larger batches, a workgroup resolves its
+ * rows once and walks every layer.  Both give identical caches. */
 size_t kvc_compact_workspace_bytes(int n_seq, int budget);
 int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_layer_ptrs,
                 const uint64_t* v_layer_ptrs, int64_t num_pages, int64_t page_stride,

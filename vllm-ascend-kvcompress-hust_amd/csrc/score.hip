@@ -529,10 +529,16 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_kernel(AggArgs a) {
   if (valid && q == 0 && !a.layer_out_stride) a.agg[tok] = finalize(total, a);
 }
 
-// Head-major scores (unit token stride): one lane per token, so every load of
-// a wave reads 64 consecutive tokens of one head (256 contiguous bytes); the
-// head maximum stays in the lane.  Heads are visited in index order.
+// Head-major scores (unit token stride): two lanes per token, the lower and
+// upper halves of a wave, each taking every other head (h = part, part + 2,
+// ...), so every load of a wave reads 32 consecutive tokens of two heads
+// (two 128-byte runs) with eight loads in flight per lane, and the two partial
+// maxima meet through one exchange across the halves.  Twice the waves of one
+// lane per token: 104 against 112 us on 4 x 131072 tokens x 6 layers x 40
+// heads, level on the smaller batches.
 constexpr int kAggHeadUnroll = 8;
+constexpr int kAggTokLanes = 2;
+constexpr int kAggTokPerBlock = kAggThreads / kAggTokLanes;
 
 __global__ __launch_bounds__(kAggThreads) void aggregate_tokens_kernel(AggArgs a) {
   extern __shared__ float dyn[];
@@ -540,10 +546,12 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_tokens_kernel(AggArgs a
   float* s_scale = dyn + a.n_layers * a.n_heads;
   const int b = blockIdx.y;
   const int n = a.seq_lens[b];
-  if (static_cast<int64_t>(blockIdx.x) * kAggThreads >= n) return;
+  if (static_cast<int64_t>(blockIdx.x) * kAggTokPerBlock >= n) return;
   load_layer_stats(a, b, s_mean, s_scale);
   __syncthreads();
-  const int t = blockIdx.x * kAggThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int part = lane >> 5;  // which half of the heads
+  const int t = blockIdx.x * kAggTokPerBlock + (threadIdx.x >> 6) * 32 + (lane & 31);
   const bool valid = t < n;
   const bool rsqrt_form = (a.flags & KVC_AGG_RSQRT) != 0;
   const int64_t tok = a.token_offsets[b] + (valid ? t : 0);
@@ -554,24 +562,28 @@ __global__ __launch_bounds__(kAggThreads) void aggregate_tokens_kernel(AggArgs a
     const float* ls = s_scale + l * a.n_heads;
     float best = -INFINITY;
     if (valid) {
-      int h = 0;
-      for (; h + kAggHeadUnroll <= a.n_heads; h += kAggHeadUnroll) {
+      int h = part;
+      for (; h + kAggTokLanes * (kAggHeadUnroll - 1) < a.n_heads; h += kAggTokLanes * kAggHeadUnroll) {
         float v[kAggHeadUnroll];
 #pragma unroll
-        for (int u = 0; u < kAggHeadUnroll; ++u) v[u] = col[(h + u) * a.raw_head_stride];
+        for (int u = 0; u < kAggHeadUnroll; ++u) v[u] = col[(h + kAggTokLanes * u) * a.raw_head_stride];
 #pragma unroll
-        for (int u = 0; u < kAggHeadUnroll; ++u)
-          best = max_nan(best, normalise(v[u], lm[h + u], ls[h + u], rsqrt_form));
+        for (int u = 0; u < kAggHeadUnroll; ++u) {
+          const int hh = h + kAggTokLanes * u;
+          best = max_nan(best, normalise(v[u], lm[hh], ls[hh], rsqrt_form));
+        }
       }
-      for (; h < a.n_heads; ++h) best = max_nan(best, normalise(col[h * a.raw_head_stride], lm[h], ls[h], rsqrt_form));
+      for (; h < a.n_heads; h += kAggTokLanes)
+        best = max_nan(best, normalise(col[h * a.raw_head_stride], lm[h], ls[h], rsqrt_form));
     }
+    best = max_nan(best, __shfl_xor(best, 32));
     if (a.layer_out_stride) {
-      if (valid) a.agg[l * a.layer_out_stride + tok] = best;
+      if (valid && part == 0) a.agg[l * a.layer_out_stride + tok] = best;
       continue;
     }
     total = combine_layers(total, best, l, a, tok);
   }
-  if (valid && !a.layer_out_stride) a.agg[tok] = finalize(total, a);
+  if (valid && part == 0 && !a.layer_out_stride) a.agg[tok] = finalize(total, a);
 }
 
 // Layer scores [n_layers][stride] -> aggregate: layers combined in layer order
@@ -915,7 +927,7 @@ int launch_aggregate(const char* who, kvc_stream_t stream, int n_layers, int n_h
   aa.layer_out_stride = layer_out_stride;
   const size_t lds = static_cast<size_t>(2) * n_layers * n_heads * sizeof(float);
   if (raw_token_stride == 1) {
-    dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggThreads)), static_cast<unsigned>(n_seq));
+    dim3 grid(static_cast<unsigned>(ceil_div(max_seq_len, kAggTokPerBlock)), static_cast<unsigned>(n_seq));
     aggregate_tokens_kernel<<<grid, kAggThreads, lds, as_stream(stream)>>>(aa);
     return launch_status(who);
   }
