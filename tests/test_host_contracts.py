@@ -377,3 +377,69 @@ def test_backward_compatible_config_alias():
 
     assert triattention.TriAttentionAscendConfig is TriAttentionConfig
     assert "TriAttentionAscendConfig" in triattention.__all__
+
+
+class _FakeEvent:
+    """Stands in for a HIP event: done when the test says so, with a set time."""
+
+    def __init__(self, clock):
+        self.clock = clock
+        self.t = None
+
+    def record(self):
+        self.t = self.clock["now"]
+
+    def query(self):
+        return self.clock["done"]
+
+    def elapsed_time(self, other):
+        return other.t - self.t
+
+
+def _drive_choice(times_ms, rows=100, done=True):
+    """Run CompactionFormChoice through its schedule with fake events; each
+    call of form f takes times_ms[f][k] for its k-th timed run."""
+    from kvcompress_mi355x.methods.triattention.pipeline import CompactionFormChoice
+
+    clock = {"now": 0.0, "done": done}
+    choice = CompactionFormChoice(event_factory=lambda: _FakeEvent(clock), capturing=lambda: False)
+    forms, count = [], {"planned": 0, "walked": 0}
+    for _ in range(len(CompactionFormChoice.SCHEDULE) + 2):
+        form, marks = choice.next_call()
+        forms.append((form, marks is not None))
+        if marks is not None:
+            marks[0].record()
+            clock["now"] += times_ms[form][count[form]]
+            count[form] += 1
+            marks[1].record()
+            choice.timed(form, marks, rows)
+    return choice, forms
+
+
+def test_compaction_form_schedule_and_margin():
+    choice, forms = _drive_choice({"planned": [4.45, 4.46], "walked": [4.30, 4.25]})
+    assert forms[:6] == [("planned", False), ("walked", False), ("planned", True), ("walked", True),
+                         ("planned", True), ("walked", True)]
+    assert choice.chosen == "walked"  # 4.25 < 0.97 * 4.45
+    assert forms[6:] == [("walked", False), ("walked", False)]
+    assert choice.per_row_ms == {"planned": 4.45 / 100, "walked": 4.25 / 100}
+
+
+def test_compaction_form_keeps_planned_inside_margin_and_when_slower():
+    assert _drive_choice({"planned": [4.45, 4.46], "walked": [4.36, 4.40]})[0].chosen == "planned"
+    assert _drive_choice({"planned": [4.45, 4.46], "walked": [5.07, 5.08]})[0].chosen == "planned"
+    # A slow first timed trial does not decide: the faster of each form's two counts.
+    assert _drive_choice({"planned": [6.0, 4.45], "walked": [4.25, 7.0]})[0].chosen == "walked"
+
+
+def test_compaction_form_waits_for_events_and_capture():
+    from kvcompress_mi355x.methods.triattention.pipeline import CompactionFormChoice
+
+    choice, forms = _drive_choice({"planned": [4.45, 4.46], "walked": [4.0, 4.0]}, done=False)
+    # Trials still in flight: the planned form runs outside the schedule.
+    assert choice.chosen is None and forms[6:] == [("planned", False), ("planned", False)]
+    # settle() decides from whatever has completed, the planned form if nothing has.
+    choice.settle()
+    assert choice.chosen == "planned"
+    captured = CompactionFormChoice(event_factory=lambda: None, capturing=lambda: True)
+    assert captured.next_call() == ("planned", None) and captured._next == 0
