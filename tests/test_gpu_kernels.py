@@ -606,13 +606,14 @@ def _layers(g, n_layers, pages, kv, dim, dtype):
     return ks, vs
 
 
-@pytest.mark.parametrize("path", ["walk", "plan"])
+@pytest.mark.parametrize("path", ["walk", "plan", "plan-interleaved"])
 @pytest.mark.parametrize("mode", ["private", "inplace"])
 @pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided", "split"])
 def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> None:
-    """Both private-mode forms (rows resolved per workgroup and every layer
-    walked, or rows planned once into the workspace and moved one layer per
-    workgroup) and the in-place walk, against the reference materialisation."""
+    """Every form (rows resolved per workgroup and every layer walked, or rows
+    planned once into the workspace and moved one layer per workgroup, layer
+    after layer or with the layers interleaved), after the ordered in-place
+    walk where the mode has one, against the reference materialisation."""
     _, _, cache = _kvc()
     from kvcompress_mi355x.methods.triattention import _device as dev
 
@@ -678,6 +679,7 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> No
         workspace=None
         if path == "walk"
         else torch.full((cache.compact_workspace_bytes(len(lens), budget),), 0xAB, dtype=torch.uint8, device=hip_device),
+        layer_order="interleaved" if path == "plan-interleaved" else "layer_major",
     )
     torch.cuda.synchronize()
     for layer in range(n_layers):
@@ -694,10 +696,10 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> No
 
 @pytest.mark.parametrize("kv,dim", [(1, 128), (4, 128), (8, 128), (10, 128)], ids=["256B", "1KB", "2KB", "2560B"])
 def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
-    """The planned private form for row widths that give 1, 2 or 8 rows per
-    128-thread workgroup and rows split into two column slices (2560 B), with
-    an unmapped destination page, bit-exact against the walked form and the
-    reference materialisation."""
+    """The planned private form (both layer orders) for row widths that give
+    1, 2 or 8 rows per 128-thread workgroup and rows split into two column
+    slices (2560 B), with an unmapped destination page, bit-exact against the
+    walked form and the reference materialisation."""
     _, _, cache = _kvc()
     from kvcompress_mi355x.methods.triattention import _device as dev
 
@@ -717,7 +719,8 @@ def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
     keeps = [torch.sort(torch.randperm(n, generator=g)[:budget]).values for n in lens]
     ks, vs = _layers(g, n_layers, pool, kv, dim, torch.bfloat16)
     results = {}
-    for path in ("walk", "plan"):
+    paths = ("walk", "plan", "plan-interleaved")
+    for path in paths:
         ks_d = [k.to(hip_device) for k in ks]
         vs_d = [v.to(hip_device) for v in vs]
         so, si, _ = dev.ragged(src_tables, hip_device)
@@ -738,6 +741,7 @@ def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
             workspace=None
             if path == "walk"
             else torch.empty(cache.compact_workspace_bytes(len(lens), budget), dtype=torch.uint8, device=hip_device),
+            layer_order="interleaved" if path == "plan-interleaved" else "layer_major",
         )
         torch.cuda.synchronize()
         results[path] = ([k.cpu() for k in ks_d], [v.cpu() for v in vs_d])
@@ -748,13 +752,14 @@ def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
         for layer in range(n_layers):
             for kind, src_cache in ((0, ks), (1, vs)):
                 want = ref.gather_paged_tokens(src_cache[layer], torch.tensor(src_tables[b]), keep_b, 128)
-                for path in ("walk", "plan"):
+                for path in paths:
                     got_cache = results[path][kind][layer].view(-1, kv, dim)
                     slots = torch.tensor([dst[i // 128] * 128 + i % 128 for i in rows])
                     assert torch.equal(got_cache[slots], want), (path, b, layer, kind)
     for kind in range(2):
         for layer in range(n_layers):
-            assert torch.equal(results["walk"][kind][layer], results["plan"][kind][layer])
+            for path in paths[1:]:
+                assert torch.equal(results["walk"][kind][layer], results[path][kind][layer])
 
 
 def test_materialize_token_slots_padded_pages(hip_device) -> None:

@@ -287,7 +287,9 @@ def test_workspace_query_and_argument_validation_without_gpu() -> None:
     with pytest.raises(ValueError, match="budget"):
         _native.call("kvc_select_keep", None, 1, 10, None, None, None, 20, 0, 0, 1, 0, None, 20)
     with pytest.raises(ValueError):
-        _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4, None, 0)
+        _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4, None, 0, 0)
+    with pytest.raises(ValueError, match="layer order"):
+        _native.call("kvc_compact", None, 1, None, None, 10, 16, 8, 2, 1, None, None, None, None, None, None, 4, 4, None, 0, 7)
 
 
 def test_max_scorer_queries_and_validation_without_gpu() -> None:
@@ -403,7 +405,7 @@ def _drive_choice(times_ms, rows=100, done=True):
 
     clock = {"now": 0.0, "done": done}
     choice = CompactionFormChoice(event_factory=lambda: _FakeEvent(clock), capturing=lambda: False)
-    forms, count = [], {"planned": 0, "walked": 0}
+    forms, count = [], {"layer_major": 0, "interleaved": 0}
     for _ in range(len(CompactionFormChoice.SCHEDULE) + 2):
         form, marks = choice.next_call()
         forms.append((form, marks is not None))
@@ -417,29 +419,29 @@ def _drive_choice(times_ms, rows=100, done=True):
 
 
 def test_compaction_form_schedule_and_margin():
-    choice, forms = _drive_choice({"planned": [4.45, 4.46], "walked": [4.30, 4.25]})
-    assert forms[:6] == [("planned", False), ("walked", False), ("planned", True), ("walked", True),
-                         ("planned", True), ("walked", True)]
-    assert choice.chosen == "walked"  # 4.25 < 0.97 * 4.45
-    assert forms[6:] == [("walked", False), ("walked", False)]
-    assert choice.per_row_ms == {"planned": 4.45 / 100, "walked": 4.25 / 100}
+    choice, forms = _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [4.30, 4.25]})
+    assert forms[:6] == [("layer_major", False), ("interleaved", False), ("layer_major", True), ("interleaved", True),
+                         ("layer_major", True), ("interleaved", True)]
+    assert choice.chosen == "interleaved"  # 4.25 < 0.97 * 4.45
+    assert forms[6:] == [("interleaved", False), ("interleaved", False)]
+    assert choice.per_row_ms == {"layer_major": 4.45 / 100, "interleaved": 4.25 / 100}
 
 
 def test_compaction_form_keeps_planned_inside_margin_and_when_slower():
-    assert _drive_choice({"planned": [4.45, 4.46], "walked": [4.36, 4.40]})[0].chosen == "planned"
-    assert _drive_choice({"planned": [4.45, 4.46], "walked": [5.07, 5.08]})[0].chosen == "planned"
+    assert _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [4.36, 4.40]})[0].chosen == "layer_major"
+    assert _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [5.07, 5.08]})[0].chosen == "layer_major"
     # A slow first timed trial does not decide: the faster of each form's two counts.
-    assert _drive_choice({"planned": [6.0, 4.45], "walked": [4.25, 7.0]})[0].chosen == "walked"
+    assert _drive_choice({"layer_major": [6.0, 4.45], "interleaved": [4.25, 7.0]})[0].chosen == "interleaved"
 
 
 def test_compaction_form_waits_for_events_and_capture():
     from kvcompress_mi355x.methods.triattention.pipeline import CompactionFormChoice
 
-    choice, forms = _drive_choice({"planned": [4.45, 4.46], "walked": [4.0, 4.0]}, done=False)
+    choice, forms = _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [4.0, 4.0]}, done=False)
     # Trials still in flight: the planned form runs outside the schedule.
-    assert choice.chosen is None and forms[6:] == [("planned", False), ("planned", False)]
+    assert choice.chosen is None and forms[6:] == [("layer_major", False), ("layer_major", False)]
     # settle() decides from whatever has completed, the planned form if nothing has.
     choice.settle()
-    assert choice.chosen == "planned"
+    assert choice.chosen == "layer_major"
     captured = CompactionFormChoice(event_factory=lambda: None, capturing=lambda: True)
-    assert captured.next_call() == ("planned", None) and captured._next == 0
+    assert captured.next_call() == ("layer_major", None) and captured._next == 0

@@ -228,14 +228,20 @@ __global__ void compact_plan_kernel(CompactArgs a, int64_t* __restrict__ plan) {
   plan[2 * idx + 1] = m.dst;
 }
 
-// Planned private mode, second launch: a workgroup moves the K and V words of
-// one row tile x one column slice of one sequence in one layer.  Grid order:
-// sequence fastest, then slice, tile, and layer slowest.
+// Planned mode, second launch: a workgroup moves the K and V words of one row
+// tile x one column slice of one sequence in one layer.  Grid order: sequence
+// fastest, then slice and tile, within groups of `lgrp` layers whose
+// workgroups interleave (layer fastest): lgrp = 1 runs the layers one after
+// the other, lgrp = n_layers keeps every layer's buffers in flight at once.
 template <typename Chunk>
 __global__ __launch_bounds__(kPlanThreads) void compact_layer_kernel(CompactArgs a, const int64_t* __restrict__ plan,
-                                                                     int64_t per_layer) {
-  const int layer = static_cast<int>(blockIdx.x / per_layer);
-  const int64_t bx = blockIdx.x - static_cast<int64_t>(layer) * per_layer;
+                                                                     int64_t per_layer, int lgrp) {
+  const int64_t group_wgs = per_layer * lgrp;
+  const int group = static_cast<int>(blockIdx.x / group_wgs);
+  const int64_t within = blockIdx.x - static_cast<int64_t>(group) * group_wgs;
+  const int lg = min(lgrp, a.n_layers - group * lgrp);  // layers in this group
+  const int layer = group * lgrp + static_cast<int>(within % lg);
+  const int64_t bx = within / lg;
   const int b = static_cast<int>(bx % a.n_seq);
   const int64_t rest = bx / a.n_seq;
   const int slice = static_cast<int>(rest % a.n_slices);
@@ -414,10 +420,12 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
                            const int64_t* src_block_offsets, const int64_t* src_block_ids,
                            const int64_t* dst_block_offsets, const int64_t* dst_block_ids,
                            const int64_t* keep, int64_t keep_stride, int budget, void* workspace,
-                           size_t workspace_bytes) {
+                           size_t workspace_bytes, int order) {
   if (n_layers <= 0 || n_layers > 65535 || n_seq <= 0 || n_seq > 65535)
     return fail(KVC_EINVAL, "kvc_compact: bad layer or sequence count");
   if (elem_bytes != 2) return fail(KVC_EINVAL, "kvc_compact: elem_bytes must be 2");
+  if (order != KVC_COMPACT_LAYER_MAJOR && order != KVC_COMPACT_LAYERS_INTERLEAVED)
+    return fail(KVC_EINVAL, "kvc_compact: unknown layer order %d", order);
   if (row_elems <= 0 || budget <= 0 || keep_stride < budget || num_pages <= 0)
     return fail(KVC_EINVAL, "kvc_compact: bad sizes");
   if (page_stride < row_elems * kBlockSize)
@@ -508,11 +516,12 @@ extern "C" int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_
     compact_plan_kernel<<<static_cast<unsigned>(ceil_div(rows, 256)), 256, 0, st>>>(ca, plan);
     if (int rc = launch_status("kvc_compact(plan)")) return rc;
     const unsigned grid = static_cast<unsigned>(per_layer * n_layers);
+    const int lgrp = order == KVC_COMPACT_LAYERS_INTERLEAVED ? n_layers : 1;
     switch (word) {
-      case 16: compact_layer_kernel<w128><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer); break;
-      case 8: compact_layer_kernel<w64><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer); break;
-      case 4: compact_layer_kernel<uint32_t><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer); break;
-      default: compact_layer_kernel<uint16_t><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer); break;
+      case 16: compact_layer_kernel<w128><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer, lgrp); break;
+      case 8: compact_layer_kernel<w64><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer, lgrp); break;
+      case 4: compact_layer_kernel<uint32_t><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer, lgrp); break;
+      default: compact_layer_kernel<uint16_t><<<grid, kPlanThreads, 0, st>>>(ca, plan, per_layer, lgrp); break;
     }
     return launch_status("kvc_compact");
   }

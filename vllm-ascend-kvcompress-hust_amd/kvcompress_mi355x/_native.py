@@ -14,7 +14,7 @@ from pathlib import Path
 LIBRARY_NAME = "libkvcompress_mi355x.so"
 LIBRARY_PATH = Path(__file__).resolve().parent / LIBRARY_NAME
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 EINVAL = -22
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -30,6 +30,8 @@ AGG_FINALIZE = 2
 AGG_RSQRT = 4
 RAW_TOKEN_MAJOR = 0
 RAW_HEAD_MAJOR = 1
+COMPACT_LAYER_MAJOR = 0
+COMPACT_LAYERS_INTERLEAVED = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -84,7 +86,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "kvc_compact_workspace_bytes": (_sz, [_i32, _i32]),
     "kvc_compact": (
         _i32,
-        [_p, _i32, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _sz],
+        [_p, _i32, _p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _sz, _i32],
     ),
     "kvc_rewrite_block_tables": (_i32, [_p, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]),
     "kvc_token_slots": (_i32, [_p, _p, _i64, _p, _i64, _i32, _p]),

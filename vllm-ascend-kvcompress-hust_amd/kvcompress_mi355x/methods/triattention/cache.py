@@ -139,13 +139,19 @@ def compact_layers(
     keep: torch.Tensor,
     budget: int,
     workspace: torch.Tensor | None = None,
+    layer_order: str = "layer_major",
 ) -> None:
     """Move every layer's kept K/V rows (``dst_block_ids`` None = in place).
 
     ``workspace`` (uint8, at least :func:`compact_workspace_bytes`) lets a
-    private-destination batch of up to 32 sequences resolve its rows once and
-    move them one layer per workgroup; without it every workgroup walks all
-    layers.  The caches end up identical either way."""
+    batch of up to 32 sequences resolve its rows once and move them one layer
+    per workgroup (in place: the rows after the ordered walk), dispatched
+    ``layer_order`` = "layer_major" (one layer after the other) or
+    "interleaved" (every layer's workgroups interleaved); without it every
+    workgroup walks all layers.  The caches end up identical either way."""
+    orders = {"layer_major": _native.COMPACT_LAYER_MAJOR, "interleaved": _native.COMPACT_LAYERS_INTERLEAVED}
+    if layer_order not in orders:
+        raise ValueError(f"unknown layer order {layer_order!r}")
     n_layers = int(k_layer_ptrs.numel())
     if int(v_layer_ptrs.numel()) != n_layers:
         raise ValueError("K and V layer tables differ in length")
@@ -171,6 +177,7 @@ def compact_layers(
         int(budget),
         dev.ptr(workspace),
         0 if workspace is None else int(workspace.numel() * workspace.element_size()),
+        orders[layer_order],
     )
 
 

@@ -518,11 +518,9 @@ class CompressionPipeline:
         return self.keep[: batch.n_seq]
 
     def compact(self, batch: Batch) -> None:
-        """kvc_compact over every layer.  The first two calls on this cache
-        run the planned form (row offsets in the workspace) and the walked
-        form (no workspace) once each with HIP events; once both have
-        completed, the faster per moved row is used from then on (see
-        CompactionFormChoice).  Both forms write identical caches."""
+        """kvc_compact over every layer, in the layer order this cache's
+        trials chose (CompactionFormChoice).  Every order writes identical
+        caches."""
         form, marks = self.compaction_form.next_call(self.device)
         if marks is not None:
             marks[0].record()
@@ -539,16 +537,17 @@ class CompressionPipeline:
             dst_block_ids=batch.dst_ids,
             keep=self.keep,
             budget=self.budget,
-            workspace=self.compact_ws if form == "planned" else None,
+            workspace=self.compact_ws,
+            layer_order=form,
         )
         if marks is not None:
             marks[1].record()
             self.compaction_form.timed(form, marks, batch.n_seq * self.budget)
 
     def settle_compaction(self, batch: Batch) -> str:
-        """Run the compaction form trials on this batch now and wait for them
-        (the calls compact's first steps on a new cache would otherwise make
-        lazily); returns the form kept.  The batch's destinations are written
+        """Run the compaction layer-order trials on this batch now and wait
+        for them (the calls compact's first steps on a new cache would
+        otherwise make lazily); returns the order kept.  The batch's destinations are written
         as by any compaction (in place: the front pages are re-compacted)."""
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("settle_compaction waits for its trials and cannot run under graph capture")
@@ -615,26 +614,27 @@ class CompressionPipeline:
 
 
 class CompactionFormChoice:
-    """Which kvc_compact form a pipeline uses for its cache.
+    """Which layer order a pipeline's planned compaction uses for its cache.
 
-    The planned form (a workspace: row offsets resolved once, then one layer
-    per workgroup) and the walked form (no workspace: a workgroup walks every
-    layer of its rows) move the same bytes, but their speed depends on where
-    the cache's pages sit in HBM, which is fixed for the life of the cache
-    and invisible to the kernels: on the Qwen2.5-14B 16 x 16384 batch, over
-    fresh allocations of the same pool, the planned form ran 4.40 - 4.47 ms in
-    every one and the walked form 4.24 - 5.08 ms.  The first two calls on a
-    cache run one form each untimed (first touches), the next four alternate
-    the forms with HIP events on the stream, read back later without waiting;
-    once all four have completed, the walked form is kept if its faster trial
-    moved a row at least 3% faster than the planned form's, else the planned
-    form.  Until then, and under graph capture, the planned form runs outside
-    the trial schedule.
+    kvc_compact's planned copy moves the same bytes in either order, but
+    which is faster depends on where the cache's pages sit in HBM, which is
+    fixed for the life of the cache and invisible to the kernels: on the
+    Qwen2.5-14B 16 x 16384 batch, over fresh allocations of the same pool,
+    one layer at a time ran 4.40 - 4.48 ms in every one, every layer
+    interleaved 4.15 - 4.17 ms in some and 4.65 - 5.04 ms in others (the
+    walked form, 4.24 - 5.09 ms, follows the interleaved one a little
+    behind).  The first two calls on a cache run one order each untimed
+    (first touches), the next four alternate the orders with HIP events on
+    the stream, read back later without waiting; once all four have
+    completed, the interleaved order is kept if its faster trial moved a row
+    at least 3% faster than the layer-major order's, else the layer-major
+    order.  Until then, and under graph capture, the layer-major order runs
+    outside the trial schedule.
     """
 
-    FORMS = ("planned", "walked")
-    SCHEDULE = (("planned", False), ("walked", False), ("planned", True), ("walked", True), ("planned", True),
-                ("walked", True))
+    FORMS = ("layer_major", "interleaved")
+    SCHEDULE = (("layer_major", False), ("interleaved", False), ("layer_major", True), ("interleaved", True),
+                ("layer_major", True), ("interleaved", True))
     MARGIN = 0.97
 
     def __init__(self, event_factory=None, capturing=None) -> None:
@@ -651,7 +651,7 @@ class CompactionFormChoice:
         if self.chosen is not None:
             return self.chosen, None
         if self._capturing():
-            return "planned", None
+            return "layer_major", None
         self._decide()
         if self.chosen is not None:
             return self.chosen, None
@@ -661,17 +661,17 @@ class CompactionFormChoice:
             if not timed:
                 return form, None
             return form, (self._event(), self._event())
-        return "planned", None  # timed trials still in flight
+        return "layer_major", None  # timed trials still in flight
 
     def timed(self, form: str, marks: tuple, rows: int) -> None:
         self._trials.append((form, marks, max(int(rows), 1)))
 
     def settle(self) -> None:
         """Decide now, after the caller has synchronised the device with every
-        trial run (the planned form if the schedule did not complete)."""
+        trial run (the layer-major order if the schedule did not complete)."""
         self._decide()
         if self.chosen is None:
-            self.chosen = "planned"
+            self.chosen = "layer_major"
 
     def _decide(self) -> None:
         n_timed = sum(1 for _, timed in self.SCHEDULE if timed)
@@ -682,7 +682,7 @@ class CompactionFormChoice:
             ms = m[0].elapsed_time(m[1]) / rows
             best[form] = min(best.get(form, ms), ms)
         self.per_row_ms = best
-        self.chosen = "walked" if best["walked"] < self.MARGIN * best["planned"] else "planned"
+        self.chosen = "interleaved" if best["interleaved"] < self.MARGIN * best["layer_major"] else "layer_major"
         self._trials.clear()
 
 
