@@ -293,11 +293,11 @@ int kvc_select_keep_split(kvc_stream_t stream, int n_seq, int max_seq_len, const
  * rows once and walks every layer.  All forms give identical caches.
  * order: the dispatch order of the planned copy's per-layer workgroups,
  * KVC_COMPACT_LAYER_MAJOR (one layer after the other: few buffers in flight)
- * or KVC_COMPACT_LAYERS_INTERLEAVED (the layers' workgroups interleaved:
- * every layer's buffers in flight at once).  Which is faster depends on where
- * the cache's pages sit in HBM (Qwen2.5-14B 16 x 16384 over fresh
- * allocations: 4.40-4.48 ms layer-major in all, interleaved 4.15-4.17 ms in
- * some and 4.65-5.04 ms in others), so a caller may time both on its cache.
+ * or KVC_COMPACT_LAYERS_INTERLEAVED (layer fastest, then row tile, sequence
+ * slowest: every layer's buffers in flight at once).  Which is faster depends
+ * on where the cache's pages sit in HBM (Qwen2.5-14B 16 x 16384 over fresh
+ * allocations: layer-major 4.37-4.49 ms in all, interleaved 4.12-4.24 ms in
+ * some and 4.59-4.77 ms in others), so a caller may time both on its cache.
  * The walked form ignores it. */
 size_t kvc_compact_workspace_bytes(int n_seq, int budget);
 int kvc_compact(kvc_stream_t stream, int n_layers, const uint64_t* k_layer_ptrs,

@@ -619,11 +619,9 @@ class CompactionFormChoice:
     kvc_compact's planned copy moves the same bytes in either order, but
     which is faster depends on where the cache's pages sit in HBM, which is
     fixed for the life of the cache and invisible to the kernels: on the
-    Qwen2.5-14B 16 x 16384 batch, over fresh allocations of the same pool,
-    one layer at a time ran 4.40 - 4.48 ms in every one, every layer
-    interleaved 4.15 - 4.17 ms in some and 4.65 - 5.04 ms in others (the
-    walked form, 4.24 - 5.09 ms, follows the interleaved one a little
-    behind).  The first two calls on a cache run one order each untimed
+    Qwen2.5-14B 16 x 16384 batch, over five fresh allocations of the same
+    pool, one layer at a time ran 4.37 - 4.49 ms in every one, every layer
+    interleaved 4.12 - 4.24 ms in three and 4.59 - 4.77 ms in two.  The first two calls on a cache run one order each untimed
     (first touches), the next four alternate the orders with HIP events on
     the stream, read back later without waiting; once all four have
     completed, the interleaved order is kept if its faster trial moved a row
