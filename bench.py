@@ -526,7 +526,7 @@ def measure(spec, args) -> dict:
     # Pipeline set-up, untimed: the compaction form for this cache's
     # placement in HBM is chosen from timed trials of both forms.
     pipeline.select_step(batch)
-    pipeline.settle_compaction(batch)
+    pipeline.settle_compaction(batch, repeat_in_place=True)  # in place: the front pages are restored below
     if restore is not None:
         restore()
     torch.cuda.synchronize()

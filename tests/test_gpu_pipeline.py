@@ -263,3 +263,42 @@ def test_pipeline_reused_with_a_smaller_batch(hip_device) -> None:
             torch.testing.assert_close(mean[s_idx, 0].cpu(), want_mean.reshape(-1), rtol=1e-4, atol=1e-4)
             torch.testing.assert_close(var[s_idx, 0].cpu(), want_var.reshape(-1), rtol=1e-3, atol=1e-4)
         assert_keep_matches(keep, out["keep"], out["agg"], spec.budget, _protected(n, spec))
+
+
+@pytest.mark.parametrize("order", ["layer_major", "interleaved"])
+def test_compaction_order_choice_and_forced_order(hip_device, order) -> None:
+    """settle_compaction times both layer orders and keeps one of them; a
+    step in either order compacts bit-exactly (the check of _run_and_check
+    after the order is forced), and an in-place batch is refused unless the
+    caller accepts repeated compaction."""
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(2, n_layers=3, score_layer_stride=2, seq_lens=(3000, 5000, 2100), budget=2048,
+                                 recent=128, max_model_len=16384)
+    cache = workloads.move_cache(workloads.build_synthetic_cache(spec, "cpu", seed=1), hip_device)
+    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline.select_step(batch)
+    chosen = pipeline.settle_compaction(batch)
+    assert chosen in ("layer_major", "interleaved")
+    assert set(pipeline.compaction_form.per_row_ms) == {"layer_major", "interleaved"}
+
+    import kvcompress_mi355x.methods.triattention.pipeline as pl
+
+    original = pl.CompactionFormChoice.__init__
+
+    def forced(self, *args, **kwargs):
+        original(self, *args, **kwargs)
+        self.chosen = order
+
+    pl.CompactionFormChoice.__init__ = forced
+    try:
+        _run_and_check(spec, hip_device)
+    finally:
+        pl.CompactionFormChoice.__init__ = original
+
+    ispec = workloads.config_spec(4, n_layers=2, score_layer_stride=1, seq_lens=(6000,), pool_pages=60, max_model_len=16384)
+    icache = workloads.move_cache(workloads.build_synthetic_cache(ispec, "cpu", seed=2), hip_device)
+    ipipe, ibatch = workloads.build_pipeline(icache)
+    ipipe.select_step(ibatch)
+    with pytest.raises(ValueError, match="repeat_in_place"):
+        ipipe.settle_compaction(ibatch)

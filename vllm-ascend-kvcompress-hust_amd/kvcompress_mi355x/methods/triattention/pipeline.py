@@ -544,13 +544,19 @@ class CompressionPipeline:
             marks[1].record()
             self.compaction_form.timed(form, marks, batch.n_seq * self.budget)
 
-    def settle_compaction(self, batch: Batch) -> str:
+    def settle_compaction(self, batch: Batch, *, repeat_in_place: bool = False) -> str:
         """Run the compaction layer-order trials on this batch now and wait
         for them (the calls compact's first steps on a new cache would
-        otherwise make lazily); returns the order kept.  The batch's destinations are written
-        as by any compaction (in place: the front pages are re-compacted)."""
+        otherwise make lazily); returns the order kept.  Each trial is a full
+        compaction of the batch: with private destinations that rewrites the
+        same destination rows every time, but in place the second trial would
+        compact an already compacted cache, so an in-place batch is refused
+        unless ``repeat_in_place`` says the caller restores its pages (or
+        does not need them) afterwards."""
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("settle_compaction waits for its trials and cannot run under graph capture")
+        if batch.inplace and not repeat_in_place:
+            raise ValueError("settle_compaction repeats the compaction: an in-place batch needs repeat_in_place=True")
         choice = self.compaction_form
         for _ in range(len(choice.SCHEDULE)):
             if choice.chosen is not None:
