@@ -172,20 +172,24 @@ def test_score_paged_matches_oracle(hip_device, case) -> None:
 MAX_CASES = [
     # (kv, qpk, head_dim, rotary, style, dtype, tokens, max_model_len -> offsets)
     (8, 5, 128, 128, "half", torch.bfloat16, 1000, 32768),        # 16 offsets, one chunk
-    (8, 5, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: a chunk per head + a shared tail chunk
+    (8, 5, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: a chunk per head + one tail chunk (two quads)
     (4, 8, 128, 128, "half", torch.bfloat16, 700, 131072),        # 18: two chunks per head, two head groups
-    (4, 5, 128, 128, "half", torch.bfloat16, 900, 65536),         # 17: tail rows of one offset, 16 heads a chunk
-    (2, 3, 128, 64, "half", torch.bfloat16, 800, 1 << 23),        # 24: two heads per tail chunk, two tail chunks
-    (2, 1, 128, 128, "half", torch.bfloat16, 400, 1 << 20),       # 21: one query head, partly filled tail chunk
-    (2, 5, 128, 64, "interleaved", torch.bfloat16, 500, 1 << 23),  # 24: three tail chunks, partial RoPE
-    (2, 8, 128, 64, "half", torch.bfloat16, 300, 1 << 23),        # 24: four tail chunks, LDS exactly full
+    (4, 5, 128, 128, "half", torch.bfloat16, 900, 65536),         # 17: tail rows of one offset, two quads a chunk
+    (2, 3, 128, 64, "half", torch.bfloat16, 800, 1 << 23),        # 24: two chunks per head (no tail past 20)
+    (2, 1, 128, 128, "half", torch.bfloat16, 400, 1 << 20),       # 21: one query head, two chunks
+    (2, 5, 128, 64, "interleaved", torch.bfloat16, 500, 1 << 23),  # 24: two chunks per head, partial RoPE
+    (2, 8, 128, 64, "half", torch.bfloat16, 300, 1 << 23),        # 24: two chunks per head, eight heads
     (2, 4, 128, 128, "half", torch.bfloat16, 5000, 32768),        # several spans per workgroup
-    (2, 8, 256, 64, "half", torch.bfloat16, 700, 262144),         # partial RoPE, 19 offsets (two tail chunks)
+    (2, 8, 256, 64, "half", torch.bfloat16, 700, 262144),         # partial RoPE, 19 offsets (one quad a tail chunk: two)
     (8, 5, 128, 128, "half", torch.float16, 513, 32768),
     (8, 5, 128, 128, "interleaved", torch.bfloat16, 600, 131072),
     (2, 8, 256, 64, "interleaved", torch.float16, 300, 32768),
     (2, 4, 64, 64, "half", torch.bfloat16, 257, 8),               # 4 offsets
     (1, 8, 256, 256, "half", torch.bfloat16, 130, 65536),         # F = 128: one query head per workgroup
+    (8, 5, 128, 128, "half", torch.bfloat16, 600, 1 << 19),       # 20: one quad a tail chunk, two tail chunks
+    (2, 8, 128, 64, "half", torch.bfloat16, 500, 65536),          # 17: two full quads share one tail chunk
+    (2, 3, 128, 128, "half", torch.bfloat16, 450, 65536),         # 17: one partly filled quad
+    (4, 4, 128, 64, "interleaved", torch.bfloat16, 700, 32768),   # 16: one tile per pass, partial RoPE
     # vector-ALU path: F not a multiple of 32 or head_dim not 64/128/256
     (4, 4, 128, 32, "half", torch.bfloat16, 400, 32768),          # F = 16, partial RoPE
     (2, 6, 96, 96, "interleaved", torch.float16, 350, 131072),    # F = 48, 18 offsets

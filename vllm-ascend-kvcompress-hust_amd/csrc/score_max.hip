@@ -11,21 +11,25 @@
 // the keys the B operand of v_mfma_f32_16x16x32_{bf16,f16}; a B operand lane
 // holds the same eight key values as an A operand lane of the mean scorer
 // (token l%16, dims 8*(l/16)..+8 of the K step), so the key loads are shared.
-// D[4*kb + i][t] is then offset 4*kb + i of token t: the maximum over a chunk
-// is three in-lane maxima and two exchanges across the four row blocks.  The
-// magnitude and pass terms do not depend on the offset: they come from the
-// mean scorer's fragments (rotary weights zero) in the same transposed form,
-// D[4*kb + i][t] = query head 4*kb + i, and are added after the maximum, as
-// in the reference.
+// D[4*kb + i][t] is then offset 4*kb + i of token t.  The maximum over a
+// query head's offsets is taken in two steps: in-lane over the four rows of a
+// lane's row block (per head of a quad of four heads), then over the four
+// row blocks by one reduce-scatter per quad (two v_permlane32_swap, one
+// v_permlane16_swap and three maxima), which leaves head 4*q + kb of quad q
+// in row block kb.  The magnitude and pass terms do not depend on the offset:
+// they come from the mean scorer's fragments (rotary weights zero) in the
+// same transposed form, rows permuted so that D[4*kb + i][t] = query head
+// 4*i + kb, the head the reduce-scatter leaves in that lane for quad i, and
+// are added after the maximum, as in the reference.
 //
 // Work split: a workgroup owns one KV head, a group of its query heads (all of
 // them when their fragments fit the LDS budget) and kMaxSpans consecutive
 // 256-token spans; its four waves walk interleaved 16-token tiles of a span.
 // The per-offset fragments (bf16 or fp16 hi/lo, 1 KB per 32 rotary dims and
 // chunk) are staged in LDS once per workgroup; each fragment read feeds two
-// key tiles.  Workgroups that share a key span but not a query-head group are
-// placed eight apart in the grid, on the same XCD, so the second read of the
-// keys is an L2 hit.  Raw scores and partial sums have the mean scorer's
+// key tiles (one in the three-waves-per-SIMD form).  Workgroups that share a
+// key span but not a query-head group are placed eight apart in the grid, on
+// the same XCD, so the second read of the keys is an L2 hit.  Raw scores and partial sums have the mean scorer's
 // layout, so kvc_head_stats and kvc_aggregate are shared.
 
 #include <math.h>
@@ -126,10 +130,12 @@ __global__ __launch_bounds__(256) void fold_offsets_kernel(OffsetFoldArgs m) {
 }
 
 // Tail chunks: one thread per (sequence, layer, KV head, tail chunk, step,
-// operand lane).  Row j of chunk tc is offset 16 + j % R of query head
-// tc * HT + j / R; rows past the chunk's heads repeat its first row (their
-// values are never part of a maximum).
-__global__ __launch_bounds__(256) void fold_offsets_tail_bf16_kernel(OffsetFoldArgs m, int tail_r, int tail_ht,
+// operand lane).  Row 4*rb + i of chunk tc holds query head 4*quad + i at
+// offset 16 + oi: with two quads of heads a chunk (R <= 2 tail offsets),
+// quad = 2*tc + rb/2 and oi = min(rb % 2, R - 1); with one (R = 3, 4),
+// quad = tc and oi = min(rb, R - 1).  Heads past the last repeat it (rows
+// whose maximum is never stored), as do offsets past the last.
+__global__ __launch_bounds__(256) void fold_offsets_tail_bf16_kernel(OffsetFoldArgs m, int tail_r, int tail_qpc,
                                                                      int tail_n, int64_t tail_base) {
   typedef MfmaElem<false> E;
   const FoldArgs& a = m.f;
@@ -146,11 +152,12 @@ __global__ __launch_bounds__(256) void fold_offsets_tail_bf16_kernel(OffsetFoldA
   const int layer = static_cast<int>(r % a.n_layers);
   const int b = static_cast<int>(r / a.n_layers);
   const int j = lane & 15, kb = lane >> 4;
-  int hl = j / tail_r, jj = j - (j / tail_r) * tail_r;
-  if (hl >= tail_ht || tc * tail_ht + hl >= a.qpk) hl = jj = 0;
-  const int g = tc * tail_ht + hl;
+  const int rb = j >> 2;  // row block of D
+  const int quad = tail_qpc == 2 ? 2 * tc + (rb >> 1) : tc;
+  const int oi = min(tail_qpc == 2 ? (rb & 1) : rb, tail_r - 1);
+  const int g = min(4 * quad + (j & 3), a.qpk - 1);
   const int64_t row = (static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + g;
-  const int o = 16 + jj;
+  const int o = 16 + oi;
   u32x4 hi, lo;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -216,26 +223,35 @@ struct MaxGeometry {
   int groups;  // query-head groups per KV head
   int nch;     // 16-offset chunks per query head
   int work;    // (span set, KV head) items
-  // Shared tail chunks (16 < offsets <= 24, bf16): offsets 16.. of tail_ht
-  // query heads per chunk, tail_r rows each; tail_n chunks per KV head, at
-  // tail_base (16-byte words) in the fragment region.
-  int tail_r, tail_ht, tail_n;
+  // Shared tail chunks (16 < offsets <= 20, bf16): offsets 16.. of the query
+  // heads in quads, tail_qpc quads per chunk, tail_r rows each; tail_n chunks
+  // per KV head, at tail_base (16-byte words) in the fragment region.
+  int tail_r, tail_qpc, tail_n;
   int64_t tail_base;
 };
 
-template <int NK, int NF, int NCH, bool F16, bool IL>
-__global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, MaxGeometry geo, int qpk,
-                                                                  const u32x4* __restrict__ rest_frags,
-                                                                  const float* __restrict__ rest_scale,
-                                                                  const u32x4* __restrict__ off_frags,
-                                                                  const float* __restrict__ off_scale) {
+// One tile per fragment pass at three waves per SIMD, or two tiles per pass
+// at two: the first keeps more key loads in flight, the second halves the
+// fragment reads per product.
+template <int NK, bool ONE_TILE>
+struct MaxTiling {
+  static constexpr int T = ONE_TILE || NK >= 8 ? 1 : 2;
+  static constexpr int kWavesPerSimd = ONE_TILE ? 3 : 1;  // 1: no request
+};
+
+template <int NK, int NF, int NCH, bool F16, bool IL, bool ONE_TILE>
+__global__ __launch_bounds__(kScoreThreads)
+__attribute__((amdgpu_waves_per_eu(MaxTiling<NK, ONE_TILE>::kWavesPerSimd))) void score_max_kernel(
+    ScoreArgs a, MaxGeometry geo, int qpk, const u32x4* __restrict__ rest_frags, const float* __restrict__ rest_scale,
+    const u32x4* __restrict__ off_frags, const float* __restrict__ off_scale) {
   typedef MfmaElem<F16> E;
   typedef typename E::vec vec_t;
   constexpr int NR = 2 * NF;   // rotary K steps of 32 dims
   constexpr int NP = NK - NR;  // pass K steps
   constexpr int kNP = NP > 0 ? NP : 1;
   constexpr int kStreams = kScoreThreads / 64;
-  extern __shared__ u32x4 lds_frag[];  // [gpg][NCH][NR][hi/lo][64]
+  constexpr int kQuads = kMfmaMaxQpk / 4;  // quads of query heads in a group
+  extern __shared__ u32x4 lds_frag[];      // [gpg][NCH][NR][hi/lo][64], then the tail chunks
 
   // blockIdx.x = ((item / 8) * groups + group) * 8 + item % 8: the groups of
   // one item are eight workgroups apart (same XCD).
@@ -277,12 +293,15 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
   }
 
   // Magnitude and pass fragments (packed [frag][kb][g < qpk], rotary weights
-  // zero), used as A operands: lane (kb, r) holds row r = query head.
+  // zero) as A operands.  Row r takes local query head 4*(r%4) + r/4, so D row
+  // 4*kb + i holds local head 4*i + kb: the head that the reduction below
+  // leaves in row block kb of quad i.
   constexpr int kFrags = 2 * NK + 2 * NF;
   const int packed = 4 * qpk;
-  const bool live_row = r < qpk;
+  const int r_head = 4 * (r & 3) + (r >> 2);
+  const bool live_row = r_head < gcnt;
   const u32x4* fp = rest_frags + (((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * kFrags) * packed +
-                    kb * qpk + (live_row ? r : 0);
+                    kb * qpk + (live_row ? g0 + r_head : 0);
   auto frag_word = [&](int f) {
     const u32x4 v = fp[f * packed];
     return __builtin_bit_cast(vec_t, live_row ? v : u32x4{0, 0, 0, 0});
@@ -298,15 +317,20 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     m_hi[q] = frag_word(2 * NK + 2 * q);
     m_lo[q] = frag_word(2 * NK + 2 * q + 1);
   }
-  // Output heads of this lane: D rows 4*kb + i.  fp16 column scales per head.
-  float r_scale[4], o_scale[4];
-  bool writes[4];
+
+  // Score stage: one row per query head of the group and a spare row that
+  // takes the stores of lanes without a head in the group.  In quad q this
+  // lane's output is local head 4*q + kb (fp16: with its column scales).
+  __shared__ __attribute__((aligned(16))) float stage[(kMfmaMaxQpk + 1) * kStageStride];
+  float r_scale[kQuads], o_scale[kQuads];
+  float* stage_rows[kQuads];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = 4 * kb + i;
-    writes[i] = h >= g0 && h < g0 + gcnt;
-    r_scale[i] = F16 && h < qpk ? rest_scale[col0 + h] : 1.0f;
-    o_scale[i] = F16 && h < qpk ? off_scale[col0 + h] : 1.0f;
+  for (int q = 0; q < kQuads; ++q) {
+    const int lh = 4 * q + kb;
+    const bool writes = lh < gcnt;
+    r_scale[q] = F16 && writes ? rest_scale[col0 + g0 + lh] : 1.0f;
+    o_scale[q] = F16 && writes ? off_scale[col0 + g0 + lh] : 1.0f;
+    stage_rows[q] = stage + (writes ? lh : kMfmaMaxQpk) * kStageStride + r;
   }
 
   KVC_GLOBAL const uint16_t* kbase = gptr_from_int<const uint16_t>(a.k_layer_ptrs[layer]);
@@ -316,16 +340,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
   const int64_t lane_off = static_cast<int64_t>(head) * a.head_dim + 8 * kb;
   const int64_t tok_base = a.token_offsets[b];
   float* raw_out = a.raw + layer * a.raw_layer_stride;
-
-  // Score stage: one row per query head of the group and a spare row that
-  // takes the stores of lanes without a head in the group.
-  __shared__ __attribute__((aligned(16))) float stage[(kMfmaMaxQpk + 1) * kStageStride];
-  float* stage_rows[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) stage_rows[i] = stage + (writes[i] ? 4 * kb + i - g0 : kMfmaMaxQpk) * kStageStride + r;
   __syncthreads();  // fragments staged
 
-  // Magnitude + pass term of a tile: D[4*kb + i][r] = query head 4*kb + i, token r.
+  // Magnitude + pass term of a tile: D[4*kb + i][r] = local query head 4*i + kb, token r.
   auto rest_tile = [&](const u32x4 (&ka)[NK]) {
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -351,19 +368,6 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     return acc0 + acc1;
   };
 
-  // D[4*kb + i][r] of one offset chunk holds offset 16c + 4*kb + i of token r:
-  // the maximum over a chunk is three in-lane maxima and two exchanges across
-  // the row blocks.  v_permlane32_swap / v_permlane16_swap of a value with
-  // itself leave lanes l and l^32 (l^16) holding the pair {x_l, x_(l^32)} in
-  // some order, so a maximum of the two results is the exchange-and-max.
-  auto token_max = [&](const f32x4& v) {
-    float m = max_prop(max_prop(v[0], v[1]), max_prop(v[2], v[3]));
-    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    m = max_prop(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
-    const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    return max_prop(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
-  };
-
   // Keys of a 16-token tile of the span starting at token st0.  Tiles past the
   // span re-read its last tile and rows past the sequence read whatever their
   // page holds: a token is a column of every product here, so those rows only
@@ -384,15 +388,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
 
   // Wave w scores tiles w, w+4, w+8, w+12 of every span in groups of T tiles
   // (T = 2: each fragment read feeds two tiles; T = 1 for head_dim 256,
-  // whose key registers would otherwise leave one wave per SIMD: 0.52 against
-  // 0.69 ms on the Qwen3.5 shape, while T = 2 is 6% faster at head_dim 128).
-  // The keys of the next group, also across a span boundary and the span's
-  // epilogue, are in flight while a group is scored.
-  constexpr int T = NK >= 8 ? 1 : 2;
+  // whose key registers would otherwise leave one wave per SIMD, and for the
+  // three-waves-per-SIMD form).  The keys of the next group, also across a
+  // span boundary and the span's epilogue, are in flight while a group is
+  // scored.
+  constexpr int T = MaxTiling<NK, ONE_TILE>::T;
   constexpr int kGroups = 4 / T;
   static_assert(kScoreTile == 16 * 4 * kStreams, "four tiles per wave cover a span");
   static_assert(kGroups % 2 == 0, "a span's first group lands in buffer 0");
   const int n_sp = min(kMaxSpans, (n - tile_first * kScoreTile + kScoreTile - 1) / kScoreTile);
+  const int n_items = gcnt * NCH;  // one item = one 16-offset chunk of one query head
+  const bool tail_pair = geo.tail_qpc == 2;
   u32x4 kbuf[2][T][NK];
   SpanPages pages;
   pages.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, tile_first * kScoreTile);
@@ -410,71 +416,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
     const bool more = sp + 1 < n_sp;
     SpanPages next;  // pages past the table resolve as missing; unused after the last span
     next.resolve(kbase, bt, n_blocks, a.num_pages, a.page_stride, t0 + kScoreTile);
-    // Column 16*mt + r of the lane's four head rows (columns past the span
-    // are never read back).
-    auto emit = [&](int mt, const f32x4& v) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) stage_rows[i][mt * 16] = v[i];
-    };
 
-    // T tiles per pass over the staged fragments.  The maximum of query head
-    // g is reduced while the MFMAs of head g + 1 run.
     auto score_group = [&](int mt_first, const u32x4 (&kk)[T][NK]) {
-      f32x4 rest[T], mx[T], pend[T], best[T];
-#pragma unroll
-      for (int u = 0; u < T; ++u) {
-        rest[u] = rest_tile(kk[u]);
-        mx[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        pend[u] = mx[u];
-      }
-      int pend_g = -1;  // no lane takes head -1
-      auto retire = [&]() {
-#pragma unroll
-        for (int u = 0; u < T; ++u) {
-          const float v = token_max(pend[u]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mx[u][i] = (4 * kb + i == pend_g) ? v : mx[u][i];
-        }
-      };
-      // One item = one 16-offset chunk of one query head: 2*NR fragment
-      // reads and 2*NR*T MFMAs.  Items alternate between two register buffers
-      // so the next item's fragments are read while this item's MFMAs run.
-      auto item = [&](auto parity, int it, const vec_t (&w)[2 * NR]) {
-        constexpr int P = decltype(parity)::value;
-        f32x4 acc[T][2];
-#pragma unroll
-        for (int u = 0; u < T; ++u) acc[u][0] = acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int st = 0; st < NR; ++st) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int u = 0; u < T; ++u) {
-              // T = 2: two chains (one per tile) each take hi then lo;
-              // T = 1: hi and lo go to separate chains, summed at the end.
-              const int chain = T == 1 ? h : 0;
-              acc[u][chain] = E::mfma(w[2 * st + h], __builtin_bit_cast(vec_t, kk[u][st]), acc[u][chain]);
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < T; ++u) {
-          const f32x4 v = T == 1 ? acc[u][0] + acc[u][1] : acc[u][0];
-          if constexpr (NCH == 1 || P == 0) {
-            best[u] = v;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) best[u][i] = max_prop(best[u][i], v[i]);
-          }
-        }
-        if constexpr (NCH == 1 || P == 1) {
-          retire();
-#pragma unroll
-          for (int u = 0; u < T; ++u) pend[u] = best[u];
-          pend_g = g0 + it / NCH;
-        }
-      };
-      const int n_items = gcnt * NCH;
+      // Fragments of item it (clamped to the last item) from LDS.
       auto load_w = [&](int it, vec_t (&w)[2 * NR]) {
         const u32x4* wl = lds_frag + (min(it, n_items - 1) * NR) * 128 + lane;
 #pragma unroll
@@ -483,21 +427,10 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
           w[2 * st + 1] = __builtin_bit_cast(vec_t, wl[st * 128 + 64]);
         }
       };
-      vec_t wa[2 * NR], wb[2 * NR];
-      load_w(0, wa);
-      int it = 0;
-      for (; it + 1 < n_items; it += 2) {
-        load_w(it + 1, wb);
-        item(std::integral_constant<int, 0>{}, it, wa);
-        load_w(it + 2, wa);
-        item(std::integral_constant<int, 1>{}, it + 1, wb);
-      }
-      if (it < n_items) item(std::integral_constant<int, 0>{}, it, wa);  // odd count: NCH == 1 only
-      retire();
-      // Tail chunks: each head's maximum over its rows, folded into its lane's
-      // maximum over offsets 0..15.
-      for (int tc = 0; tc < (kTail ? geo.tail_n : 0); ++tc) {
-        const u32x4* wl = lds_frag + (n_items + tc) * NR * 128 + lane;
+      // Products of the 16 rows of one chunk with the T tiles: D[4*kb + i][r]
+      // = row 4*kb + i, token r.  T = 2: one chain per tile, hi then lo;
+      // T = 1: hi and lo in separate chains, summed at the end.
+      auto chunk_products = [&](const vec_t (&w)[2 * NR], f32x4 (&res)[T]) {
         f32x4 acc[T][2];
 #pragma unroll
         for (int u = 0; u < T; ++u) acc[u][0] = acc[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -505,40 +438,115 @@ __global__ __launch_bounds__(kScoreThreads) void score_max_kernel(ScoreArgs a, M
         for (int st = 0; st < NR; ++st) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const vec_t w = __builtin_bit_cast(vec_t, wl[st * 128 + h * 64]);
 #pragma unroll
             for (int u = 0; u < T; ++u) {
               const int chain = T == 1 ? h : 0;
-              acc[u][chain] = E::mfma(w, __builtin_bit_cast(vec_t, kk[u][st]), acc[u][chain]);
+              acc[u][chain] = E::mfma(w[2 * st + h], __builtin_bit_cast(vec_t, kk[u][st]), acc[u][chain]);
             }
           }
         }
-        for (int hl = 0; hl < geo.tail_ht; ++hl) {
-          const int g = tc * geo.tail_ht + hl;
-          if (g >= qpk) break;  // the same for every lane
-          const int lo_row = hl * geo.tail_r, hi_row = lo_row + geo.tail_r;
 #pragma unroll
-          for (int u = 0; u < T; ++u) {
-            const f32x4 v = T == 1 ? acc[u][0] + acc[u][1] : acc[u][0];
-            f32x4 mine;
+        for (int u = 0; u < T; ++u) res[u] = T == 1 ? acc[u][0] + acc[u][1] : acc[u][0];
+      };
+      auto max4 = [](const f32x4& v) { return max_prop(max_prop(v[0], v[1]), max_prop(v[2], v[3])); };
+
+      f32x4 rest[T];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int row = 4 * kb + i;
-              mine[i] = row >= lo_row && row < hi_row ? v[i] : -INFINITY;
+      for (int u = 0; u < T; ++u) rest[u] = rest_tile(kk[u]);
+      // Fragment registers: two buffers (the next item's fragments are read
+      // while this item's products run), or, in the one-tile form, one buffer
+      // whose words are replaced by the next item's as their products issue.
+      constexpr int kBufs = ONE_TILE ? 1 : 2;
+      vec_t wbuf[kBufs][2 * NR];
+      load_w(0, wbuf[0]);
+      f32x4 tv[T];
+      float outv[T][kQuads];
+#pragma unroll
+      for (int q = 0; q < kQuads; ++q) {
+#pragma unroll
+        for (int u = 0; u < T; ++u) outv[u][q] = 0.0f;
+        if (4 * q >= gcnt) continue;  // the same for every lane
+        // P[u][j]: maximum over the offsets in this lane's row block (D rows
+        // 4*kb .. 4*kb + 3 of each chunk) for local head 4*q + j, tile u.
+        float P[T][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            const int it = (4 * q + j) * NCH + c;
+            if (4 * q + j < gcnt) {
+              f32x4 res[T];
+              if constexpr (ONE_TILE) {
+                const u32x4* wl = lds_frag + (min(it + 1, n_items - 1) * NR) * 128 + lane;
+                f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+                for (int st = 0; st < NR; ++st) {
+#pragma unroll
+                  for (int h = 0; h < 2; ++h) {
+                    acc[h] = E::mfma(wbuf[0][2 * st + h], __builtin_bit_cast(vec_t, kk[0][st]), acc[h]);
+                    wbuf[0][2 * st + h] = __builtin_bit_cast(vec_t, wl[st * 128 + h * 64]);
+                  }
+                }
+                res[0] = acc[0] + acc[1];
+              } else {
+                load_w(it + 1, wbuf[(it + 1) & 1]);
+                chunk_products(wbuf[it & 1], res);
+              }
+#pragma unroll
+              for (int u = 0; u < T; ++u) {
+                const float m = max4(res[u]);
+                P[u][j] = c == 0 ? m : max_prop(P[u][j], m);
+              }
+            } else {
+#pragma unroll
+              for (int u = 0; u < T; ++u) P[u][j] = -INFINITY;
             }
-            const float tmax = token_max(mine);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx[u][i] = (4 * kb + i == g) ? max_prop(mx[u][i], tmax) : mx[u][i];
           }
+        }
+        if constexpr (kTail) if (geo.tail_n > 0) {
+          // Tail rows of head 4*q + j are element j of row blocks 2*(q%2) and
+          // 2*(q%2) + 1 (two quads a chunk) or of every row block (one).
+          if (q == 0 || !tail_pair) {
+            vec_t w[2 * NR];
+            const u32x4* wl = lds_frag + (n_items + (tail_pair ? 0 : q)) * NR * 128 + lane;
+#pragma unroll
+            for (int st = 0; st < NR; ++st) {
+              w[2 * st] = __builtin_bit_cast(vec_t, wl[st * 128]);
+              w[2 * st + 1] = __builtin_bit_cast(vec_t, wl[st * 128 + 64]);
+            }
+            chunk_products(w, tv);
+          }
+          const bool take = !tail_pair || (kb >> 1) == (q & 1);
+#pragma unroll
+          for (int u = 0; u < T; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) P[u][j] = max_prop(P[u][j], take ? tv[u][j] : -INFINITY);
+        }
+        // Maximum over the four row blocks, scattered so that row block kb
+        // ends with head 4*q + kb.  v_permlane32_swap(x, y) returns the lower
+        // half of x then of y (lanes l and l + 32 of x in lower lane l, of y
+        // in upper lane l + 32) and the upper halves; v_permlane16_swap does
+        // the same for rows 0/1 and 2/3 of each half.  The maximum of each
+        // pair is therefore a maximum over two row blocks of one head.
+#pragma unroll
+        for (int u = 0; u < T; ++u) {
+          const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(P[u][0]), __float_as_uint(P[u][2]), false, false);
+          const float x02 = max_prop(__uint_as_float(s02[0]), __uint_as_float(s02[1]));
+          const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(P[u][1]), __float_as_uint(P[u][3]), false, false);
+          const float x13 = max_prop(__uint_as_float(s13[0]), __uint_as_float(s13[1]));
+          const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x02), __float_as_uint(x13), false, false);
+          outv[u][q] = max_prop(__uint_as_float(s[0]), __uint_as_float(s[1]));
         }
       }
+      // Column 16*mt + r of the lane's head rows (columns past the span are
+      // never read back).
 #pragma unroll
       for (int u = 0; u < T; ++u) {
-        f32x4 out;
+        const int mt = mt_first + kStreams * u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          out[i] = F16 ? mx[u][i] * o_scale[i] + rest[u][i] * r_scale[i] : mx[u][i] + rest[u][i];
-        emit(mt_first + kStreams * u, out);
+        for (int q = 0; q < kQuads; ++q)
+          stage_rows[q][mt * 16] =
+              F16 ? outv[u][q] * o_scale[q] + rest[u][q] * r_scale[q] : outv[u][q] + rest[u][q];
       }
     };
 
@@ -761,22 +769,26 @@ ValuMaxKernel pick_valu_max(int nch) {
 using MaxKernel = void (*)(ScoreArgs, MaxGeometry, int, const u32x4*, const float*, const u32x4*, const float*);
 
 template <int NCH, bool F16, bool IL>
-MaxKernel pick_max_chunks(int nk, int nf) {
+MaxKernel pick_max_chunks(int nk, int nf, bool one_tile) {
+  if (one_tile) {  // head_dim 128, one chunk per query head, no tail chunks
+    if (NCH != 1 || nk != 4) return nullptr;
+    return nf == 1 ? score_max_kernel<4, 1, 1, F16, IL, true> : nf == 2 ? score_max_kernel<4, 2, 1, F16, IL, true> : nullptr;
+  }
   switch (nk * 16 + nf) {
-    case 2 * 16 + 1: return score_max_kernel<2, 1, NCH, F16, IL>;
-    case 4 * 16 + 1: return score_max_kernel<4, 1, NCH, F16, IL>;
-    case 4 * 16 + 2: return score_max_kernel<4, 2, NCH, F16, IL>;
-    case 8 * 16 + 1: return score_max_kernel<8, 1, NCH, F16, IL>;
-    case 8 * 16 + 2: return score_max_kernel<8, 2, NCH, F16, IL>;
-    case 8 * 16 + 4: return score_max_kernel<8, 4, NCH, F16, IL>;
+    case 2 * 16 + 1: return score_max_kernel<2, 1, NCH, F16, IL, false>;
+    case 4 * 16 + 1: return score_max_kernel<4, 1, NCH, F16, IL, false>;
+    case 4 * 16 + 2: return score_max_kernel<4, 2, NCH, F16, IL, false>;
+    case 8 * 16 + 1: return score_max_kernel<8, 1, NCH, F16, IL, false>;
+    case 8 * 16 + 2: return score_max_kernel<8, 2, NCH, F16, IL, false>;
+    case 8 * 16 + 4: return score_max_kernel<8, 4, NCH, F16, IL, false>;
     default: return nullptr;
   }
 }
 
 template <bool F16, bool IL>
-MaxKernel pick_max_typed(int nk, int nf, int nch) {
-  if (nch == 1) return pick_max_chunks<1, F16, IL>(nk, nf);
-  if (nch == 2) return pick_max_chunks<2, F16, IL>(nk, nf);
+MaxKernel pick_max_typed(int nk, int nf, int nch, bool one_tile) {
+  if (nch == 1) return pick_max_chunks<1, F16, IL>(nk, nf, one_tile);
+  if (nch == 2) return pick_max_chunks<2, F16, IL>(nk, nf, one_tile);
   return nullptr;
 }
 
@@ -791,7 +803,7 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   if (geo.nch > 2)
     return fail(KVC_EINVAL, "kvc_score_paged_max: at most 32 offsets (got %d; 2^0 .. 2^30 are 31)", n_offsets);
   int nch = geo.nch;
-  geo.tail_r = geo.tail_ht = geo.tail_n = 0;
+  geo.tail_r = geo.tail_qpc = geo.tail_n = 0;
   geo.tail_base = 0;
   if (!mfma_scorer_supported(s, dtype, fa.interleaved ? KVC_ROPE_INTERLEAVED : KVC_ROPE_HALF)) {
     const size_t lds = sizeof(float) * (2 * static_cast<size_t>(16 * nch) * s.freq + s.freq + s.pass);
@@ -806,23 +818,31 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
     vk<<<grid, 256, lds, stream>>>(sa, fa, s.qpk, n_offsets);
     return launch_status("kvc_score_paged_max");
   }
-  // 17 to 24 offsets (bf16): each query head keeps one 16-offset chunk and the
-  // remaining 1-8 offsets of several heads share tail chunks, when every head
-  // of the KV head then fits one workgroup (18 offsets, 5 query heads, 128
-  // dims: 6 chunk passes per tile instead of 10, and keys read once).
+  // 17 to 20 offsets (bf16): each query head keeps one 16-offset chunk and the
+  // remaining 1-4 offsets of its quad of heads share tail chunks (two quads a
+  // chunk for 1-2 remaining offsets), when every head of the KV head then fits
+  // one workgroup (18 offsets, 5 query heads, 128 dims: 6 chunk passes per
+  // tile instead of 10, and keys read once).
   const int64_t cols_total = static_cast<int64_t>(s.n_seq) * s.n_layers * s.kv_heads * s.qpk;
-  if (!f16 && nk >= 4 && n_offsets > 16 && n_offsets <= 24) {
-    const int r = n_offsets - 16, ht = 16 / r, tn = (s.qpk + ht - 1) / ht;
+  if (!f16 && nk >= 4 && n_offsets > 16 && n_offsets <= 20) {
+    const int r = n_offsets - 16, qpc = r <= 2 ? 2 : 1;
+    const int tn = ((s.qpk + 3) / 4 + qpc - 1) / qpc;
     if ((s.qpk + tn) * nr * 2 * kOffsetFragBytes <= kMaxFragLds) {
       geo.nch = nch = 1;
       geo.tail_r = r;
-      geo.tail_ht = ht;
+      geo.tail_qpc = qpc;
       geo.tail_n = tn;
       geo.tail_base = cols_total * nr * 128;
     }
   }
-  MaxKernel kern = f16 ? (fa.interleaved ? pick_max_typed<true, true>(nk, nf, nch) : pick_max_typed<true, false>(nk, nf, nch))
-                       : (fa.interleaved ? pick_max_typed<false, true>(nk, nf, nch) : pick_max_typed<false, false>(nk, nf, nch));
+  // One tile per pass at three waves per SIMD where that measured faster: 128
+  // dims with one chunk per query head and no tail (16 offsets, Qwen2.5-14B
+  // shape: 1.03 against 1.13 ms; with a tail chunk it is 9% slower).
+  const bool one_tile = nk == 4 && nch == 1 && geo.tail_n == 0;
+  MaxKernel kern =
+      f16 ? (fa.interleaved ? pick_max_typed<true, true>(nk, nf, nch, one_tile) : pick_max_typed<true, false>(nk, nf, nch, one_tile))
+          : (fa.interleaved ? pick_max_typed<false, true>(nk, nf, nch, one_tile)
+                            : pick_max_typed<false, false>(nk, nf, nch, one_tile));
   if (!kern) return fail(KVC_EINVAL, "kvc_score_paged_max: no scorer for head_dim %d rotary_dim %d", s.head_dim, s.rotary_dim);
   const int per_g = geo.nch * nr * 2 * kOffsetFragBytes;
   int gpg = kMaxFragLds / per_g;
@@ -867,7 +887,7 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   if (int rc = launch_status("kvc_score_paged_max(fold)")) return rc;
   if (geo.tail_n > 0) {
     fold_offsets_tail_bf16_kernel<<<static_cast<unsigned>(tail_items / 256), 256, 0, stream>>>(
-        m, geo.tail_r, geo.tail_ht, geo.tail_n, geo.tail_base);
+        m, geo.tail_r, geo.tail_qpc, geo.tail_n, geo.tail_base);
     if (int rc = launch_status("kvc_score_paged_max(tail fold)")) return rc;
   }
 
