@@ -329,9 +329,9 @@ def test_max_scorer_queries_and_validation_without_gpu() -> None:
 
 def test_max_scorer_rejects_oversized_fold_before_launch() -> None:
     """A bf16 shape whose per-offset weight fold would need more work-items than
-    one dispatch holds (4096 sequences x 64 layers x 8 KV heads x 5 query heads,
-    32 offsets: 5.4e9 fold threads) is rejected with KVC_EINVAL by the host
-    check, which runs before any launch."""
+    one dispatch holds (8192 sequences x 64 layers x 8 KV heads x 5 query heads:
+    one 256-thread workgroup per column, 5.4e9 fold threads) is rejected with
+    KVC_EINVAL by the host check, which runs before any launch."""
     import torch
 
     from kvcompress_mi355x import _native
@@ -339,7 +339,7 @@ def test_max_scorer_rejects_oversized_fold_before_launch() -> None:
     if torch.cuda.is_available():
         pytest.skip("placeholder pointers: run where no device could be reached by a launch")
     lib = _native.load()
-    n_layers, kv, head_dim, qpk, n_seq, max_len, n_off = 64, 8, 128, 5, 4096, 256, 32
+    n_layers, kv, head_dim, qpk, n_seq, max_len, n_off = 64, 8, 128, 5, 8192, 256, 32
     ws = lib.kvc_score_max_workspace_bytes(n_layers, kv, head_dim, head_dim, qpk, n_seq, max_len, n_off)
     assert ws > 0
     fake = 4096

@@ -181,18 +181,21 @@ __device__ __attribute__((aligned(16))) uint32_t kZeroKeys[8 * 16];
 // (one v_maximum3_f32 on gfx950).
 __device__ __forceinline__ float max_prop(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
-// bf16 fragments need no per-column scale: one thread per (column, chunk and
-// step, operand lane) writes that lane's hi and lo words.
+// bf16 fragments need no per-column scale.  One workgroup per column
+// (sequence, layer, KV head, query head g): its threads first fold the
+// weights of every (offset, frequency) with loads along the frequencies into
+// an LDS table [offset][rotary dim] (the same expressions as offset_weight),
+// then each (chunk and step, operand lane) reads its eight weights from the
+// table and writes its hi and lo words.  The table holds n_offsets rows of
+// 2F + 4 floats (the padding spreads a lane group's rows over the LDS banks),
+// sized by the launch so that small tables leave room for many workgroups.
+__device__ __forceinline__ int fold_table_stride(int freq) { return 2 * freq + 4; }
 __global__ __launch_bounds__(256) void fold_offsets_bf16_kernel(OffsetFoldArgs m) {
   typedef MfmaElem<false> E;
   const FoldArgs& a = m.f;
-  const int n_pos = m.nch * m.nr;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t cols = static_cast<int64_t>(a.n_seq) * a.n_layers * a.kv_heads * a.qpk;
-  if (idx >= cols * n_pos * 64) return;
-  const int lane = static_cast<int>(idx & 63);
-  const int p = static_cast<int>((idx >> 6) % n_pos);
-  const int64_t col = (idx >> 6) / n_pos;
+  extern __shared__ __attribute__((aligned(16))) float table[];  // [n_offsets][2F + 4]
+  const int kFoldStride = fold_table_stride(a.freq);
+  const int64_t col = blockIdx.x;
   const int g = static_cast<int>(col % a.qpk);
   int64_t r = col / a.qpk;
   const int head = static_cast<int>(r % a.kv_heads);
@@ -200,22 +203,38 @@ __global__ __launch_bounds__(256) void fold_offsets_bf16_kernel(OffsetFoldArgs m
   const int layer = static_cast<int>(r % a.n_layers);
   const int b = static_cast<int>(r / a.n_layers);
   const int64_t row = (static_cast<int64_t>(layer) * a.kv_heads + head) * a.qpk + g;
-  const int j = lane & 15, kb = lane >> 4;
-  const int c = p / m.nr, st = p - c * m.nr;
-  const int o = min(16 * c + j, m.n_offsets - 1);
-  u32x4 hi, lo;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float v0 = offset_weight(a, b, layer, row, o, m.n_offsets, 32 * st + 8 * kb + 2 * w);
-    const float v1 = offset_weight(a, b, layer, row, o, m.n_offsets, 32 * st + 8 * kb + 2 * w + 1);
-    const uint32_t h = E::pack(v0, v1);
-    hi[w] = h;
-    lo[w] = E::pack(v0 - E::lo(h), v1 - E::hi(h));
+  const int F = a.freq;
+  for (int i = threadIdx.x; i < m.n_offsets * F; i += blockDim.x) {
+    const int o = i / F, f = i - o * F;
+    const int64_t ph = b * a.phase_seq_stride + (static_cast<int64_t>(layer) * m.n_offsets + o) * F + f;
+    const int64_t q = row * F + f;
+    const float qr = a.q_real[q], qi = a.q_imag[q], sc = a.scale[q];
+    const float c = a.phase_cos[ph], sn = a.phase_sin[ph];
+    float* t = table + o * kFoldStride;
+    t[a.interleaved ? 2 * f : f] = sc * (qr * c - qi * sn);
+    t[a.interleaved ? 2 * f + 1 : F + f] = sc * (qi * c + qr * sn);
   }
-  u32x4* dst = m.frags + (col * n_pos * 2 + 2 * p) * 64 + lane;
-  dst[0] = hi;
-  dst[64] = lo;
-  if (p == 0 && lane == 0) m.inv_scale[col] = 1.0f;
+  __syncthreads();
+  const int n_pos = m.nch * m.nr;
+  u32x4* dst = m.frags + col * n_pos * 2 * 64;
+  for (int idx = threadIdx.x; idx < n_pos * 64; idx += blockDim.x) {
+    const int lane = idx & 63, p = idx >> 6;
+    const int j = lane & 15, kb = lane >> 4;
+    const int c = p / m.nr, st = p - c * m.nr;
+    const int o = min(16 * c + j, m.n_offsets - 1);
+    const float* src = table + o * kFoldStride + 32 * st + 8 * kb;
+    u32x4 hi, lo;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float v0 = src[2 * w], v1 = src[2 * w + 1];
+      const uint32_t h = E::pack(v0, v1);
+      hi[w] = h;
+      lo[w] = E::pack(v0 - E::lo(h), v1 - E::hi(h));
+    }
+    dst[(2 * p) * 64 + lane] = hi;
+    dst[(2 * p + 1) * 64 + lane] = lo;
+  }
+  if (threadIdx.x == 0) m.inv_scale[col] = 1.0f;
 }
 
 struct MaxGeometry {
@@ -858,9 +877,11 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   if (gx > 0x7fffffff) return fail(KVC_EINVAL, "kvc_score_paged_max: grid too large");
   // Every fold this call launches, checked before the first of them: the
   // magnitude/pass fold, the per-offset fold (fp16: one wave per column, four
-  // per workgroup; bf16: one thread per fragment lane) and the tail fold.
-  const int64_t offset_items =
-      f16 ? ceil_div(cols_total, 4) * 256 : ceil_div(cols_total * geo.nch * nr * 64, 256) * 256;
+  // per workgroup; bf16: one workgroup per column) and the tail fold.
+  // bf16 fold: one workgroup per column, its offset table in LDS (at most 32
+  // offsets x 260 floats here: 33 KB).
+  const size_t fold_lds = static_cast<size_t>(n_offsets) * (2 * s.freq + 4) * sizeof(float);
+  const int64_t offset_items = f16 ? ceil_div(cols_total, 4) * 256 : cols_total * 256;
   const int64_t tail_items =
       geo.tail_n > 0 ? ceil_div(cols_total / s.qpk * geo.tail_n * nr * 64, 256) * 256 : 0;
   const int64_t fold_items = std::max(mfma_fold_items(s, dtype), std::max(offset_items, tail_items));
@@ -883,7 +904,7 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   if (f16)
     fold_offsets_kernel<true><<<static_cast<unsigned>(offset_items / 256), 256, 0, stream>>>(m);
   else
-    fold_offsets_bf16_kernel<<<static_cast<unsigned>(offset_items / 256), 256, 0, stream>>>(m);
+    fold_offsets_bf16_kernel<<<static_cast<unsigned>(offset_items / 256), 256, fold_lds, stream>>>(m);
   if (int rc = launch_status("kvc_score_paged_max(fold)")) return rc;
   if (geo.tail_n > 0) {
     fold_offsets_tail_bf16_kernel<<<static_cast<unsigned>(tail_items / 256), 256, 0, stream>>>(
