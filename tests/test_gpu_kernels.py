@@ -189,6 +189,8 @@ MAX_CASES = [
     (8, 5, 128, 128, "half", torch.bfloat16, 600, 1 << 19),       # 20: one quad a tail chunk, two tail chunks
     (2, 8, 128, 64, "half", torch.bfloat16, 500, 65536),          # 17: two full quads share one tail chunk
     (2, 3, 128, 128, "half", torch.bfloat16, 450, 65536),         # 17: one partly filled quad
+    (2, 1, 128, 128, "half", torch.bfloat16, 333, 65536),         # 17: one query head, three empty quad slots
+    (2, 7, 128, 64, "half", torch.bfloat16, 610, 262144),         # 19: second tail chunk holds a 3-head quad
     (4, 4, 128, 64, "interleaved", torch.bfloat16, 700, 32768),   # 16: one tile per pass, partial RoPE
     # vector-ALU path: F not a multiple of 32 or head_dim not 64/128/256
     (4, 4, 128, 32, "half", torch.bfloat16, 400, 32768),          # F = 16, partial RoPE
