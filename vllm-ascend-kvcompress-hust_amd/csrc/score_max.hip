@@ -189,7 +189,7 @@ __device__ __forceinline__ float max_prop(float a, float b) { return __builtin_e
 // table and writes its hi and lo words.  The table holds n_offsets rows of
 // 2F + 4 floats (the padding spreads a lane group's rows over the LDS banks),
 // sized by the launch so that small tables leave room for many workgroups.
-__device__ __forceinline__ int fold_table_stride(int freq) { return 2 * freq + 4; }
+__host__ __device__ __forceinline__ int fold_table_stride(int freq) { return 2 * freq + 4; }
 __global__ __launch_bounds__(256) void fold_offsets_bf16_kernel(OffsetFoldArgs m) {
   typedef MfmaElem<false> E;
   const FoldArgs& a = m.f;
@@ -294,9 +294,10 @@ __attribute__((amdgpu_waves_per_eu(MaxTiling<NK, ONE_TILE>::kWavesPerSimd))) voi
   const int kb = lane >> 4;  // K block of the operands, row block of D
   const int64_t col0 = ((static_cast<int64_t>(b) * a.n_layers + layer) * a.kv_heads + head) * qpk;
   constexpr int kFragPerG = NCH * NR * 2 * 64;
-  // Shared tail chunks exist for head_dim >= 128 only: at 64 dims their code
-  // would cost the kernel its third wave per SIMD.
-  constexpr bool kTail = NCH == 1 && !F16 && NK >= 4;
+  // Shared tail chunks exist for head_dim >= 128 only (at 64 dims their code
+  // would cost the kernel its third wave per SIMD), and not in the one-tile
+  // form, which the launcher picks only without them.
+  constexpr bool kTail = NCH == 1 && !F16 && NK >= 4 && !ONE_TILE;
 
   // Stage this group's per-offset fragments.
   {
@@ -880,7 +881,7 @@ int launch_max_scorer(hipStream_t stream, const ScoreShape& s, int dtype, int n_
   // per workgroup; bf16: one workgroup per column) and the tail fold.
   // bf16 fold: one workgroup per column, its offset table in LDS (at most 32
   // offsets x 260 floats here: 33 KB).
-  const size_t fold_lds = static_cast<size_t>(n_offsets) * (2 * s.freq + 4) * sizeof(float);
+  const size_t fold_lds = static_cast<size_t>(n_offsets) * fold_table_stride(s.freq) * sizeof(float);
   const int64_t offset_items = f16 ? ceil_div(cols_total, 4) * 256 : cols_total * 256;
   const int64_t tail_items =
       geo.tail_n > 0 ? ceil_div(cols_total / s.qpk * geo.tail_n * nr * 64, 256) * 256 : 0;
