@@ -627,13 +627,14 @@ class CompactionFormChoice:
     fixed for the life of the cache and invisible to the kernels: on the
     Qwen2.5-14B 16 x 16384 batch, over five fresh allocations of the same
     pool, one layer at a time ran 4.37 - 4.49 ms in every one, every layer
-    interleaved 4.12 - 4.24 ms in three and 4.59 - 4.77 ms in two.  The first two calls on a cache run one order each untimed
-    (first touches), the next four alternate the orders with HIP events on
-    the stream, read back later without waiting; once all four have
-    completed, the interleaved order is kept if its faster trial moved a row
-    at least 3% faster than the layer-major order's, else the layer-major
-    order.  Until then, and under graph capture, the layer-major order runs
-    outside the trial schedule.
+    interleaved 4.12 - 4.24 ms in three and 4.59 - 4.77 ms in two.  The
+    first two calls on a cache run one order each untimed (first touches),
+    the next four alternate the orders with HIP events on the stream, read
+    back later without waiting; once all four have completed, the
+    interleaved order is kept if its faster trial moved a row at least 3%
+    faster than the layer-major order's, else the layer-major order.  Until
+    then, and under graph capture, the layer-major order runs outside the
+    trial schedule.
     """
 
     FORMS = ("layer_major", "interleaved")
