@@ -11,13 +11,16 @@
 //  * planned (a workspace is given and the batch has at most kPlanMaxSeqs
 //    sequences): one launch resolves every kept row once (keep index -> source
 //    page -> byte offset, and the destination offset) into the workspace, then
-//    a layer-major launch moves one layer's rows per workgroup, reading the
-//    offsets instead of chasing the indices.  The workgroups in flight at any
-//    time then touch one or two layers' pages, so the translation working set
-//    stays small whatever the physical placement of the pool (moving all
-//    layers per workgroup touches every layer's buffers at once and ran
-//    4.2-5.3 ms on the Qwen2.5-14B 16 x 16384 shape depending on the
-//    placement, the layer-major form 4.15-4.47 ms on the same buffers);
+//    a second launch moves one layer's rows per workgroup, reading the
+//    offsets instead of chasing the indices, in the caller's order: layer
+//    after layer (the workgroups in flight at any time touch one or two
+//    layers' pages, so the translation working set stays small whatever the
+//    physical placement of the pool: moving all layers per workgroup touches
+//    every layer's buffers at once and ran 4.2-5.3 ms on the Qwen2.5-14B
+//    16 x 16384 shape depending on the placement, the layer-major form
+//    4.15-4.47 ms on the same buffers) or every layer's workgroups
+//    interleaved (faster in some placements, slower in others; see
+//    compact_layer_kernel);
 //  * walked: a workgroup owns a tile of rows x one column slice of one
 //    sequence, resolves the rows' offsets once and walks every layer, loading
 //    the K and V words of the tile together before storing them.  Used
