@@ -15,11 +15,12 @@
 //    the workgroup.  Right for batches of many sequences.
 //  * kvc_select_keep_split: a job's segment is cut into chunks of >= 4096 keys,
 //    one 256-thread workgroup each.  Every radix pass is a launch: workgroups
-//    add their chunk histograms into the job's histogram in the workspace and
-//    the last one to finish (a ticket counter) picks the digit; then one
-//    launch counts each chunk's keys > T and == T and one emits, each chunk
-//    starting from the counts of the chunks before it.  Right for a few long
-//    sequences, which would otherwise run on a few CUs.
+//    add their chunk histograms into the pass's histogram in the workspace;
+//    every workgroup of a later launch picks the earlier passes' digits
+//    itself from those finished histograms (no workgroup waits for another).
+//    Then one launch counts each chunk's keys > T and == T and one emits,
+//    each chunk starting from the counts of the chunks before it.  Right for
+//    a few long sequences, which would otherwise run on a few CUs.
 // Both produce the same indices.
 //
 // Segments follow select_keep_indices (tri/selection.py:108-196): the protected
@@ -353,12 +354,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
 
 // ------------------------------------------------------ split over chunks --
 
-// Per-job scratch of the split path (in the caller's workspace).
+// Per-job scratch of the split path (in the caller's workspace): the job's
+// keep count and liveness (set by the reset launch), each radix pass's
+// histogram (the chunks' atomic sums) and each chunk's counts of keys > T and
+// == T.
 struct SplitState {
-  uint32_t want, mask, need, live;
-  uint32_t ticket[4];
+  uint32_t need, live, pad[2];
   uint32_t hist[4][256];
-  uint32_t counts[kSplitMaxChunks][2];  // keys > T, == T per chunk
+  uint32_t counts[kSplitMaxChunks][2];
 };
 
 __host__ __device__ inline int64_t split_chunk_len(int64_t len) {
@@ -392,12 +395,44 @@ __global__ __launch_bounds__(kSplitThreads) void select_split_init_kernel(Select
   }
 }
 
-// grid (chunks, segments, n_seq): one radix pass.  Each workgroup adds its
-// chunk's histogram into the job's; the last to arrive picks the digit.
+// The radix prefix (want, mask) and the number of keys still needed inside
+// it after `passes` passes: each pass's digit picked from that pass's
+// histogram, complete since an earlier launch, exactly as the last pass of
+// that histogram would have picked it.  The histograms are read together,
+// then walked in LDS.  Every thread calls it; the results are in `out` (LDS)
+// on return.
+struct Threshold {
+  uint32_t want, mask, need, digit;
+};
+__device__ void derive_threshold(const SplitState* st, int passes, uint32_t (*s_hist)[256], Threshold* out) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < passes * 256; i += kSplitThreads) (&s_hist[0][0])[i] = (&st->hist[0][0])[i];
+  if (tid == 0) *out = Threshold{0u, 0u, st->need, 0u};
+  __syncthreads();
+  for (int q = 0; q < passes; ++q) {
+    if (tid < 64) {
+      const uint32_t need = out->need;  // read by every lane before one lane writes
+      pick_digit(s_hist[q], need, &out->digit, &out->need);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int shift = 24 - 8 * q;
+      out->want |= out->digit << shift;
+      out->mask |= 0xFFu << shift;
+    }
+    __syncthreads();
+  }
+}
+
+// grid (chunks, segments, n_seq): one radix pass.  Each workgroup derives the
+// prefix of the passes before (from their histograms) and adds its chunk's
+// histogram of the matching keys into the job's; no workgroup waits for
+// another inside the launch.
 __global__ __launch_bounds__(kSplitThreads) void select_split_pass_kernel(SelectArgs a, int pass) {
   __shared__ uint32_t whist[kSplitThreads / 64][256];
   __shared__ uint32_t hist[256];
-  __shared__ uint32_t s_digit, s_need, s_last;
+  __shared__ uint32_t s_prev[3][256];
+  __shared__ Threshold s_th;
   const int c = blockIdx.x, seg = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
   SplitState* st = split_state(a, b, seg);
   if (!st->live) return;  // the whole workgroup reads the same word
@@ -407,32 +442,19 @@ __global__ __launch_bounds__(kSplitThreads) void select_split_pass_kernel(Select
   if (c >= chunks) return;
   const int64_t cs = split_chunk_len(len);
   const int64_t c0 = j.s.start + c * cs, c1 = min(j.s.stop, c0 + cs);
+  derive_threshold(st, pass, s_prev, &s_th);
   const int shift = 24 - 8 * pass;
   const float* sc = a.scores + a.token_offsets[b];
-  range_histogram<kSplitThreads>(sc, c0, c1, st->want, st->mask, shift, whist, hist);
+  range_histogram<kSplitThreads>(sc, c0, c1, s_th.want, s_th.mask, shift, whist, hist);
   for (int i = tid; i < 256; i += kSplitThreads)
     if (hist[i]) atomicAdd(&st->hist[pass][i], hist[i]);
-  __threadfence();  // this workgroup's bins are visible before its ticket
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&st->ticket[pass], 1u) == static_cast<uint32_t>(chunks - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int i = tid; i < 256; i += kSplitThreads)
-    hist[i] = __hip_atomic_load(&st->hist[pass][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (tid < 64) pick_digit(hist, st->need, &s_digit, &s_need);
-  __syncthreads();
-  if (tid == 0) {
-    st->want |= s_digit << shift;
-    st->mask |= 0xFFu << shift;
-    st->need = s_need;
-  }
 }
 
 // grid (chunks, segments, n_seq): each chunk's keys > T and == T.
 __global__ __launch_bounds__(kSplitThreads) void select_split_count_kernel(SelectArgs a) {
   __shared__ uint32_t s_wave[kSplitThreads / 64];
+  __shared__ uint32_t s_prev[4][256];
+  __shared__ Threshold s_th;
   const int c = blockIdx.x, seg = blockIdx.y, b = blockIdx.z;
   SplitState* st = split_state(a, b, seg);
   if (!st->live) return;
@@ -441,7 +463,8 @@ __global__ __launch_bounds__(kSplitThreads) void select_split_count_kernel(Selec
   if (c >= split_chunks(len)) return;
   const int64_t cs = split_chunk_len(len);
   const int64_t c0 = j.s.start + c * cs, c1 = min(j.s.stop, c0 + cs);
-  const uint32_t thresh = st->want;
+  derive_threshold(st, 4, s_prev, &s_th);
+  const uint32_t thresh = s_th.want;
   const float* sc = a.scores + a.token_offsets[b];
   uint32_t g = 0, e = 0;
   for_each_key<kSplitThreads>(sc, c0, c1, [&](int64_t, uint32_t k) {
@@ -460,6 +483,8 @@ __global__ __launch_bounds__(kSplitThreads) void select_split_count_kernel(Selec
 // grid (chunks, segments, n_seq): ordered emission of each chunk.
 __global__ __launch_bounds__(kSplitThreads) void select_split_emit_kernel(SelectArgs a) {
   __shared__ uint32_t s_wave[kSplitThreads / 64];
+  __shared__ uint32_t s_prev[4][256];
+  __shared__ Threshold s_th;
   const int c = blockIdx.x, seg = blockIdx.y, b = blockIdx.z;
   SplitState* st = split_state(a, b, seg);
   if (!st->live) return;
@@ -473,8 +498,9 @@ __global__ __launch_bounds__(kSplitThreads) void select_split_emit_kernel(Select
     g0 += st->counts[i][0];
     e0 += st->counts[i][1];
   }
+  derive_threshold(st, 4, s_prev, &s_th);
   int64_t* out = a.keep + static_cast<int64_t>(b) * a.keep_stride;
-  emit_range<kSplitThreads>(a.scores + a.token_offsets[b], c0, c1, st->want, st->need, g0, e0, out, j.out_base,
+  emit_range<kSplitThreads>(a.scores + a.token_offsets[b], c0, c1, s_th.want, s_th.need, g0, e0, out, j.out_base,
                             a.budget, s_wave);
 }
 
