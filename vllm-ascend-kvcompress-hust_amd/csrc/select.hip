@@ -322,6 +322,14 @@ __device__ void emit_range(const float* sc, int64_t start, int64_t stop, uint32_
 
 // ------------------------------------------------- one workgroup per job --
 
+// Segments whose aligned body has at most kCacheTiles emission tiles (16 384
+// scores at 1024 threads) are read once: each thread keeps its words of every
+// tile in registers, in the emission's layout, and the four radix passes and
+// the emission walk those (the up to three scores before the first and after
+// the last 16-byte boundary are read again each time, as in the uncached
+// walk).
+constexpr int kCacheTiles = 2;
+
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
   __shared__ uint32_t whist[kSelThreads / 64][256];
   __shared__ uint32_t hist[256];
@@ -336,11 +344,63 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
   if (!fill_fixed(a, j, seg, out, tid, kSelThreads)) return;
   const float* sc = a.scores + a.token_offsets[b];
 
+  constexpr int64_t kTileWords = static_cast<int64_t>(kSelThreads) * kEmitWords;
+  const int64_t start = j.s.start, stop = j.s.stop;
+  const int64_t misalign = (reinterpret_cast<uintptr_t>(sc + start) >> 2) & 3;
+  const int64_t head = min((4 - misalign) & 3, stop - start);
+  const int64_t body = start + head;
+  const int64_t n4 = (stop - body) >> 2;
+  const int64_t tail0 = body + 4 * n4;
+  const f32x4* v = reinterpret_cast<const f32x4*>(sc + body);
+  const bool cached = n4 <= kCacheTiles * kTileWords;
+  uint32_t ck[kCacheTiles][kEmitWords][4];
+  bool cv[kCacheTiles][kEmitWords];
+  if (cached) {
+#pragma unroll
+    for (int t = 0; t < kCacheTiles; ++t) {
+#pragma unroll
+      for (int u = 0; u < kEmitWords; ++u) {
+        const int64_t w = t * kTileWords + static_cast<int64_t>(tid) * kEmitWords + u;
+        cv[t][u] = w < n4;
+        const f32x4 x = cv[t][u] ? v[w] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ck[t][u][q] = float_key(x[q]);
+      }
+    }
+  }
+
   uint32_t want = 0, mask = 0;
   uint32_t need = static_cast<uint32_t>(j.s.keep);
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    range_histogram<kSelThreads>(sc, j.s.start, j.s.stop, want, mask, shift, whist, hist);
+    if (cached) {
+      for (int i = tid; i < (kSelThreads / 64) * 256; i += kSelThreads) (&whist[0][0])[i] = 0;
+      __syncthreads();
+      uint32_t* mine = whist[tid >> 6];
+      auto count = [&](uint32_t k) {
+        if ((k & mask) == want) count_digit(mine, (k >> shift) & 255u);
+      };
+      for (int64_t i = start + tid; i < body; i += kSelThreads) count(float_key(sc[i]));
+#pragma unroll
+      for (int t = 0; t < kCacheTiles; ++t)
+#pragma unroll
+        for (int u = 0; u < kEmitWords; ++u)
+          if (cv[t][u]) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) count(ck[t][u][q]);
+          }
+      for (int64_t i = tail0 + tid; i < stop; i += kSelThreads) count(float_key(sc[i]));
+      __syncthreads();
+      for (int i = tid; i < 256; i += kSelThreads) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int w = 0; w < kSelThreads / 64; ++w) c += whist[w][i];
+        hist[i] = c;
+      }
+      __syncthreads();
+    } else {
+      range_histogram<kSelThreads>(sc, start, stop, want, mask, shift, whist, hist);
+    }
     if (tid < 64) pick_digit(hist, need, &s_digit, &s_need);
     __syncthreads();
     want |= s_digit << shift;
@@ -349,7 +409,57 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelectArgs a) {
     __syncthreads();
   }
   // want: the exact key of the K-th largest score; need: its ties to keep.
-  emit_range<kSelThreads>(sc, j.s.start, j.s.stop, want, need, 0u, 0u, out, j.out_base, a.budget, s_wave);
+  if (!cached) {
+    emit_range<kSelThreads>(sc, start, stop, want, need, 0u, 0u, out, j.out_base, a.budget, s_wave);
+    return;
+  }
+  // The cached emission: emit_range's walk with the tiles' words from registers.
+  const uint32_t thresh = want, need_eq = need;
+  uint32_t g_run = 0, e_run = 0;
+  auto emit = [&](int64_t i, uint32_t k, uint32_t g, uint32_t e) {
+    if (k > thresh || (k == thresh && e < need_eq)) {
+      const int64_t slot = j.out_base + g + min(e, need_eq);
+      if (slot < a.budget) out[slot] = i;
+    }
+  };
+  auto serial = [&](int64_t i0, int64_t i1) {
+    for (int64_t i = i0; i < i1; ++i) {
+      const uint32_t k = float_key(sc[i]);
+      if (tid == 0) emit(i, k, g_run, e_run);
+      g_run += k > thresh;
+      e_run += k == thresh;
+    }
+  };
+  serial(start, body);
+#pragma unroll
+  for (int t = 0; t < kCacheTiles; ++t) {
+    if (t * kTileWords >= n4) break;  // the same for every thread
+    uint32_t g = 0, e = 0;
+#pragma unroll
+    for (int u = 0; u < kEmitWords; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        g += cv[t][u] && ck[t][u][q] > thresh;
+        e += cv[t][u] && ck[t][u][q] == thresh;
+      }
+    uint32_t tile_total;
+    const uint32_t before = block_exclusive_scan<kSelThreads>(g | (e << 16), s_wave, &tile_total);
+    uint32_t gb = g_run + (before & 0xFFFFu), eb = e_run + (before >> 16);
+#pragma unroll
+    for (int u = 0; u < kEmitWords; ++u) {
+      if (!cv[t][u]) continue;
+      const int64_t i0 = body + 4 * (t * kTileWords + static_cast<int64_t>(tid) * kEmitWords + u);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        emit(i0 + q, ck[t][u][q], gb, eb);
+        gb += ck[t][u][q] > thresh;
+        eb += ck[t][u][q] == thresh;
+      }
+    }
+    g_run += tile_total & 0xFFFFu;
+    e_run += tile_total >> 16;
+  }
+  serial(tail0, stop);
 }
 
 // ------------------------------------------------------ split over chunks --
