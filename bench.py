@@ -97,6 +97,18 @@ def parse_args() -> argparse.Namespace:
         "pass: 48 layers of 4096-token bf16 query projections (40 heads x 128), one buffer per layer",
     )
     p.add_argument(
+        "--kernel-micro",
+        action="store_true",
+        help="only measure the reference's NPU kernel micro-benchmark shapes (tests/run_npu_kernel_benchmark.py): "
+        "2176 bf16 tokens, budget 2048, 8 KV heads x 5 query heads, head_dim 128, 12 offsets at round start "
+        "8192, 6 sampled layers; copy, score, phase, aggregate and position-shift calls one by one",
+    )
+    p.add_argument(
+        "--no-other-configs",
+        action="store_true",
+        help="default workload only: skip the Qwen3.5 hybrid and 4 x 131072 in-place entries of other_configs",
+    )
+    p.add_argument(
         "--tp-rank-scorer",
         action="store_true",
         help="only measure the one-layer scorer on one tensor-parallel rank's share of a Qwen3.5-35B-A3B cache: "
@@ -203,7 +215,7 @@ def tp_rank_scorer_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool
     if not no_cpu:
         from oracle import triattention_ref as ref
 
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        threads, thread_info = cpu_threads()
         torch.set_num_threads(threads)
         stats = ref.LayerStats(
             q_mean_real=q_real.cpu(), q_mean_imag=q_imag.cpu(), q_abs_mean=q_abs.cpu(),
@@ -231,6 +243,7 @@ def tp_rank_scorer_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool
             "value": round(tokens / med, 1),
             "unit": "tokens/s",
             "cores": threads,
+            **thread_info,
             "kind": "port",
             "sample": f"the whole call: the torch restatement of score_post_rope_keys over 8192-token gathered chunks "
             f"(the reference benchmark's fallback path); median of {cpu_repeats} after 1 warm-up; "
@@ -311,7 +324,7 @@ def calibration_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -
     if not no_cpu:
         from oracle import calibration_ref as cref
 
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        threads, thread_info = cpu_threads()
         torch.set_num_threads(threads)
         sample = [q.cpu() for q in projections[:4]]
 
@@ -327,11 +340,200 @@ def calibration_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -
             "value": round(len(sample) * tokens / med, 1),
             "unit": "token-layers/s",
             "cores": threads,
+            **thread_info,
             "kind": "port",
             "sample": f"4 of 48 layers ({tokens} tokens each), torch float32 restatement; median of {cpu_repeats}",
         }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def kernel_micro_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) -> int:
+    """The reference's NPU kernel micro-benchmark (tests/run_npu_kernel_benchmark.py:44-282)
+    on the same shapes and through the same wrapper names: one 2176-token
+    bf16 sequence (8 KV heads x 5 query heads, head_dim 128) in 17
+    contiguous pages, budget 2048, 12 offsets at round start 8192, 6 sampled
+    layers for the phase preparation.  Each call is timed as the reference
+    times it (wall clock over eager calls after warm-up) and as device time
+    (the call captured once as a HIP graph, replays timed with HIP events);
+    beside it the oracle's torch path for the same call on the host CPU."""
+    import torch
+
+    from kvcompress_mi355x.methods.triattention import cache as kcache
+    from kvcompress_mi355x.methods.triattention import kernels
+
+    device = torch.device("cuda:0")
+    block, tokens, budget, kv_heads, qpk, head_dim, n_blocks = 128, 2176, 2048, 8, 5, 128, 32
+    g = torch.Generator(device=device).manual_seed(20260401)
+    k_cache = torch.randn(n_blocks, block, kv_heads, head_dim, generator=g, device=device).to(torch.bfloat16)
+    v_cache = torch.randn(n_blocks, block, kv_heads, head_dim, generator=g, device=device).to(torch.bfloat16)
+    source = torch.arange(-(-tokens // block), device=device, dtype=torch.int64)
+    destination = source[: budget // block]
+    keep = torch.arange(budget, device=device, dtype=torch.int64) + (tokens - budget)
+    k_ws = torch.empty(budget, kv_heads, head_dim, device=device, dtype=torch.bfloat16)
+    v_ws = torch.empty_like(k_ws)
+    src_slots = kcache.token_slots(source, keep, block)
+    dst_slots = kcache.token_slots(destination, torch.arange(budget, device=device, dtype=torch.int64), block)
+    freq = head_dim // 2
+    shape = (kv_heads, qpk, freq)
+    q_real = torch.randn(shape, generator=g, device=device)
+    q_imag = torch.randn(shape, generator=g, device=device)
+    q_abs = torch.sqrt(q_real.square() + q_imag.square()) + 0.2
+    scale = torch.ones(shape, device=device)
+    omega = torch.logspace(0, -4, freq, device=device)
+    offsets = torch.tensor([1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048], device=device, dtype=torch.float32)
+    extra = q_abs - torch.sqrt(q_real.square() + q_imag.square() + 1e-8)
+    out = torch.empty(kv_heads, qpk, tokens, device=device, dtype=torch.float32)
+    off_cos = torch.cos(offsets.unsqueeze(1) * omega).mean(dim=0)
+    off_sin = torch.sin(offsets.unsqueeze(1) * omega).mean(dim=0)
+    layers = 6
+    layer_omega = omega.unsqueeze(0).expand(layers, -1).contiguous()
+    layer_cos = off_cos.unsqueeze(0).expand(layers, -1).contiguous()
+    layer_sin = off_sin.unsqueeze(0).expand(layers, -1).contiguous()
+    phase_cos, phase_sin = torch.empty_like(layer_omega), torch.empty_like(layer_omega)
+    kernels.prepare_mean_phase_coefficients(layer_omega, layer_cos, layer_sin, 8192, phase_cos, phase_sin)
+    kernels.score_paged_keys_mean_precomputed(k_cache, source, q_real, q_imag, scale, extra, phase_cos[0], phase_sin[0],
+                                              tokens, out, block, "half")
+    head_mean = out.mean(dim=-1)
+    head_var = out.var(dim=-1, correction=0)
+    agg = torch.empty(tokens, device=device, dtype=torch.float32)
+    positions = torch.arange(4096, device=device, dtype=torch.int64)
+    req_idx = torch.arange(4096, device=device, dtype=torch.int64) % 16
+    req_off = torch.arange(16, device=device, dtype=torch.int64) * 128
+    physical = torch.empty_like(positions)
+
+    calls = {
+        "copy": lambda: kcache.materialize_selected_tokens(k_cache, v_cache, source, destination, keep, block),
+        "copy_slots": lambda: kcache.materialize_token_slots(k_cache, v_cache, src_slots, dst_slots, k_ws, v_ws),
+        "score": lambda: kernels.score_paged_keys_mean(k_cache, source, q_real, q_imag, scale, extra, omega, off_cos,
+                                                       off_sin, 8192, tokens, out, block, "half"),
+        "score_precomputed": lambda: kernels.score_paged_keys_mean_precomputed(
+            k_cache, source, q_real, q_imag, scale, extra, phase_cos[0], phase_sin[0], tokens, out, block, "half"),
+        "phase6": lambda: kernels.prepare_mean_phase_coefficients(layer_omega, layer_cos, layer_sin, 8192, phase_cos, phase_sin),
+        "aggregate": lambda: kernels.aggregate_normalized_scores(out, head_mean, head_var, agg, tokens,
+                                                                 layer_aggregation="mean", first_layer=True),
+        "shift": lambda: kernels.shift_positions(positions, req_idx, req_off, physical),
+    }
+    row_bytes = kv_heads * head_dim * 2
+    algo_bytes = {
+        "copy": budget * row_bytes * 2 * 2, "copy_slots": budget * row_bytes * 2 * 2,
+        "score": tokens * row_bytes, "score_precomputed": tokens * row_bytes,
+        "aggregate": kv_heads * qpk * tokens * 4 + tokens * 4, "shift": 4096 * 8 * 3,
+    }
+    # materialize_selected_tokens checks its keep indices against the table on
+    # the host (a device read), as the reference's does, so it cannot be
+    # captured: its device time is taken around eager calls instead.
+    eager_only = {"copy"}
+    results = {}
+    side = torch.cuda.Stream(device=device)
+    for name, fn in calls.items():
+        for _ in range(max(1, warmup)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        wall_ms = 1000.0 * (time.perf_counter() - t0) / steps
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if name in eager_only:
+            start.record()
+            for _ in range(steps):
+                fn()
+            end.record()
+        else:
+            graph = torch.cuda.CUDAGraph()
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.graph(graph, stream=side):
+                fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(steps):
+                graph.replay()
+            end.record()
+        torch.cuda.synchronize()
+        device_ms = start.elapsed_time(end) / steps
+        entry = {"wall_ms_per_call": round(wall_ms, 5), "device_ms_per_call": round(device_ms, 5)}
+        if name in eager_only:
+            entry["device_timing"] = "HIP events around eager calls (includes the host's per-call work)"
+        if name in algo_bytes:
+            entry["hbm_frac"] = round(algo_bytes[name] / (device_ms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)
+        results[name] = entry
+    score_ms = results["score_precomputed"]["device_ms_per_call"]
+    result = {
+        "metric": "reference NPU kernel micro-benchmark shapes: tokens scored/s of one layer (precomputed phases); "
+        "per-call times of every call",
+        "value": round(tokens / (score_ms / 1000.0), 1),
+        "unit": "tokens/s",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": score_ms,
+        "higher_is_better": True,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "timing": "wall_ms_per_call: eager calls as tests/run_npu_kernel_benchmark.py times them; device_ms_per_call: "
+        "one HIP graph replay per call, HIP events on the replay stream",
+        "config": {"workload": "reference-kernel-micro-2176", "tokens": tokens, "budget": budget, "kv_heads": kv_heads,
+                   "query_heads": kv_heads * qpk, "head_dim": head_dim, "offsets": 12, "round_start": 8192,
+                   "sampled_layers": layers},
+        "calls": results,
+        "amortized_score_ms": round(score_ms + results["phase6"]["device_ms_per_call"] / layers, 5),
+    }
+    if not no_cpu:
+        from oracle import triattention_ref as ref
+
+        threads, thread_info = cpu_threads()
+        torch.set_num_threads(threads)
+        hk, hv = k_cache.cpu(), v_cache.cpu()
+        hsrc, hdst, hkeep = source.cpu(), destination.cpu(), keep.cpu()
+        stats = ref.LayerStats(q_mean_real=q_real.cpu(), q_mean_imag=q_imag.cpu(), q_abs_mean=q_abs.cpu(),
+                               freq_scale_sq=scale.square().cpu(), omega=omega.cpu(), rope_style="half", rotary_dim=head_dim)
+        hout, hmean, hvar = out.cpu(), head_mean.cpu(), head_var.cpu()
+        hoffsets = offsets.cpu()
+        hpos, hidx, hoff = positions.cpu(), req_idx.cpu(), req_off.cpu()
+        generic = {
+            "copy": lambda: ref.materialize_selected_tokens(hk, hv, hsrc, hdst, hkeep, block),
+            "score": lambda: ref.score_post_rope_keys(
+                ref.gather_paged_range(hk, hsrc, start=0, count=tokens, block_size=block), stats,
+                round_start=8192, offsets=hoffsets, aggregation="mean"),
+            "aggregate": lambda: torch.amax((hout - hmean.unsqueeze(-1)) * torch.rsqrt(hvar.unsqueeze(-1) + 1e-6), dim=(0, 1)),
+            "shift": lambda: torch.sub(hpos, hoff.index_select(0, hidx)),
+        }
+        cpu = {}
+        for name, fn in generic.items():
+            fn()
+            times = []
+            for _ in range(cpu_repeats):
+                t = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t)
+            cpu[name] = round(1000.0 * statistics.median(times), 5)
+        result["cpu_baseline"] = {
+            "value": round(tokens / (cpu["score"] / 1000.0), 1),
+            "unit": "tokens/s",
+            "cores": threads,
+            **thread_info,
+            "kind": "port",
+            "sample": f"the oracle's torch path for each call on the host CPU (generic functions of the reference "
+            f"benchmark), median of {cpu_repeats} after 1 warm-up, ms per call: {cpu}; host CPU {cpu_model()}",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_threads() -> tuple[int, dict]:
+    """Host threads for a CPU baseline and how they were chosen: every core
+    os.cpu_count() reports, capped by OMP_NUM_THREADS where that is set (the
+    GPU box exports the CPU share of one GPU there, 16, whatever the host's
+    core count)."""
+    count = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    threads = min(count, int(env)) if env and env.isdigit() and int(env) > 0 else count
+    return threads, {
+        "os_cpu_count": count,
+        "threads_rule": "os.cpu_count()" if threads == count else f"capped by OMP_NUM_THREADS={env} (the job's CPU share)",
+    }
 
 
 def cpu_model() -> str:
@@ -454,7 +656,7 @@ def cpu_baseline(cache, spec, repeats: int, score_aggregation: str = "mean") -> 
     from oracle import stats_ref
     from oracle import triattention_ref as ref
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads, thread_info = cpu_threads()
     torch.set_num_threads(threads)
     b = 0
     n = spec.seq_lens[b]
@@ -496,6 +698,7 @@ def cpu_baseline(cache, spec, repeats: int, score_aggregation: str = "mean") -> 
         "value": round(n / med, 1),
         "unit": "tokens/s",
         "cores": threads,
+        **thread_info,
         "kind": "port",
         "sample": (
             f"1 of {len(spec.seq_lens)} sequences ({n} tokens): score {len(spec.scoring_layers)} layers "
@@ -567,6 +770,8 @@ def main() -> int:
         return calibration_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
     if args.tp_rank_scorer:
         return tp_rank_scorer_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
+    if args.kernel_micro:
+        return kernel_micro_bench(args.steps, args.warmup, args.cpu_repeats, args.no_cpu_baseline)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
@@ -582,10 +787,18 @@ def main() -> int:
     tokens = spec.total_tokens
     algo = spec.algorithmic_bytes()
     compact_gbs = algo["compact"] / (m["compact_ms"] / 1000.0) / 1e9
-    traffic = None
+    # HBM bytes per kvc_compact launch from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # counter runs of this workload (a profiler run of its own, recorded in
+    # profiles/), not measured in this process.
+    traffic, traffic_source = None, None
     traffic_file = REPO / "profiles" / f"compact_traffic_config{args.config}.json"
     if traffic_file.is_file() and args.layers is None and not args.pool_pages:
-        traffic = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+        recorded = json.loads(traffic_file.read_text())
+        traffic = recorded.get("bytes_per_launch")
+        traffic_source = (
+            f"profiles/{traffic_file.name}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this workload "
+            f"(commit {recorded.get('commit', 'unrecorded')}), scaled by a 1 GiB copy; not measured in this process"
+        )
 
     result = {
         "metric": "KV tokens scored+compacted/sec at 1 GPU; achieved HBM GB/s as % of peak",
@@ -630,6 +843,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(compact_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes": algo["compact"],
             "kernel_ms": round(m["compact_ms"], 4),
             "timing": m["compact_timing"],
@@ -660,8 +874,63 @@ def main() -> int:
         }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cache, cache.spec, args.cpu_repeats, args.score_aggregation)
+    if args.config == 2 and not args.no_other_configs and args.layers is None and not args.pool_pages:
+        del cache
+        torch.cuda.empty_cache()
+        result["other_configs"] = other_configs(args)
     print(json.dumps(result), flush=True)
     return 0
+
+
+# The reference's other headline shapes, measured after the default workload:
+# the Qwen3.5-35B-A3B hybrid batch (partial RoPE, v3 quotas, 2048-token
+# scheduler pages; tests/run_npu_partial_rope_benchmark.py:35-41,
+# tests/run_npu_qwen35_transaction_benchmark.py:92) and 4 x 131072 tokens
+# compacted in place in a full pool, each step a first compaction of the
+# same cache (front pages restored between steps, untimed).
+OTHER_CONFIGS = ((3, False), (4, True))
+OTHER_STEPS, OTHER_WARMUP = 10, 2
+
+
+def other_configs(args) -> list[dict]:
+    import torch
+
+    from kvcompress_mi355x import workloads
+
+    entries = []
+    for config, restore_front in OTHER_CONFIGS:
+        spec = workloads.config_spec(config)
+        sub = argparse.Namespace(**{**vars(args), "steps": OTHER_STEPS, "warmup": OTHER_WARMUP,
+                                    "restore_front": restore_front, "graph": False, "arena": False})
+        m = measure(spec, sub)
+        del m["cache"]
+        torch.cuda.empty_cache()
+        algo = spec.algorithmic_bytes()
+        entries.append({
+            "workload": spec.name,
+            "config": config,
+            "tokens": spec.total_tokens,
+            "n_seq": len(spec.seq_lens),
+            "layers": spec.n_layers,
+            "compaction": "in-place" if spec.inplace else "private destinations",
+            "steps": OTHER_STEPS,
+            "warmup": OTHER_WARMUP,
+            "value": round(spec.total_tokens / (m["ms_per_step"] / 1000.0), 1),
+            "unit": "tokens/s",
+            "ms_per_step": round(m["ms_per_step"], 4),
+            "step_hbm": step_hbm(spec, m["ms_per_step"]),
+            "compaction_form": m["compaction_form"],
+            "compact_roofline": {
+                "kernel_ms": round(m["compact_ms"], 4),
+                "achieved": round(algo["compact"] / (m["compact_ms"] / 1000.0) / 1e9, 1),
+                "frac": round(algo["compact"] / (m["compact_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes": algo["compact"],
+            },
+            "stages_ms": {k: round(v, 4) for k, v in m["stages_ms"].items()},
+            **({"timing": "sum of per-step HIP-event times; overwritten front pages restored before each step, untimed"}
+               if restore_front else {}),
+        })
+    return entries
 
 
 if __name__ == "__main__":

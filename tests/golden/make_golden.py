@@ -24,6 +24,7 @@ sys.path.insert(0, str(REPO / "vllm-ascend-kvcompress-hust_amd"))
 sys.path.insert(0, str(REPO))
 
 from kvcompress_mi355x import workloads  # noqa: E402
+from oracle import stats_ref  # noqa: E402
 from oracle import triattention_ref as ref  # noqa: E402
 
 
@@ -34,11 +35,19 @@ def sha256(t: torch.Tensor) -> str:
 def compute() -> dict:
     spec = workloads.config_spec(1)
     host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
-    stats = host.calibration.to_device(spec.model_shape(), torch.device("cpu"))
-    layer_stats = []
-    for layer in spec.scoring_layers:
-        s = stats[layer]
-        layer_stats.append(ref.LayerStats(s.q_mean_real, s.q_mean_imag, s.q_abs_mean, s.freq_scale_sq, s.omega, s.rope_style, s.rotary_dim, s.q_pass_mean))
+    # The calibration laid out by the oracle's own restatement of the device
+    # layout (tri/stats.py:262-360), not by the product's loader.
+    model = spec.model_shape()
+    stats = stats_ref.layer_stats_for_device(
+        host.calibration.layers,
+        host.calibration.metadata,
+        num_attention_heads=model.num_attention_heads,
+        num_kv_heads=model.num_kv_heads,
+        head_dim=model.head_dim,
+        rotary_dim=model.effective_rotary_dim,
+        rope_theta=model.rope_theta,
+    )
+    layer_stats = [stats[layer] for layer in spec.scoring_layers]
     cfg = ref.MethodConfig(budget=spec.budget, recent=spec.recent, score_chunk_size=8192, score_layer_stride=1)
     out = ref.method_select(
         [host.k_caches[layer] for layer in spec.scoring_layers],
@@ -74,7 +83,8 @@ def main() -> None:
     meta = {
         "workload": r["spec"].name,
         "generator": "kvcompress_mi355x.workloads.build_synthetic_cache(config_spec(1), 'cpu', seed=0)",
-        "oracle": "oracle.triattention_ref.method_select (torch CPU restatement of the reference torch path)",
+        "oracle": "oracle.triattention_ref.method_select (torch CPU restatement of the reference torch path) "
+        "on calibration laid out by oracle.stats_ref.layer_stats_for_device",
         "torch": torch.__version__,
         "inputs": r["inputs"],
         "head_mean": [float(x) for x in r["mean"]],

@@ -214,7 +214,10 @@ def test_generator_creates_safe_model_matched_artifact(hip_device, tmp_path: Pat
     assert not list(tmp_path.glob("*.tmp"))
     artifact = CalibrationStats.load(output)
     assert artifact.validate(ModelShape("qwen2", 2, 2, 1, 4, 10000.0, False)) == ()
-    assert artifact.metadata["generator"] == calibration.GENERATOR == "kvcompress-mi355x"
+    # The reference's generator name (its loader checks provenance under that
+    # name only); this package is recorded as the producer.
+    assert artifact.metadata["generator"] == calibration.REFERENCE_GENERATOR == "vllm-ascend-kvcompress-hust"
+    assert artifact.metadata["producer"] == calibration.GENERATOR == "kvcompress-mi355x"
     assert artifact.metadata["token_count"] == 32
     assert artifact.metadata["input_source"] == calibration.BUILTIN_INPUT_SOURCE
     assert artifact.layers[0].q_mean_real.shape == (2, 2)

@@ -473,6 +473,18 @@ SELECT_CASES = [
     (1000, 1000, 0, 128, 8, "global", False),
     (300, 128, 0, 0, 8, "v3", True),
     (19, 13, 2, 2, 8, "v3", False),
+    # The single-workgroup selector keeps a segment's 16-byte words in
+    # registers up to 4096 words (16384 scores); around that edge, with an
+    # aligned start (prefix 0) and a start three scores past a 16-byte
+    # boundary (prefix 3: one head scalar before the first word).
+    (16512, 4096, 0, 128, 8, "global", False),  # exactly 4096 words
+    (16513, 4096, 0, 128, 8, "global", True),   # 4096 words + 1 tail scalar
+    (16515, 4096, 0, 128, 8, "global", False),  # 4096 words + 3 tail scalars
+    (16516, 4096, 0, 128, 8, "global", True),   # 4097 words: the uncached walk
+    (16516, 4096, 3, 128, 8, "global", False),  # head scalar + 4096 words
+    (16519, 4096, 3, 128, 8, "global", True),   # head + 4096 words + 3 tail scalars
+    (16520, 4096, 3, 128, 8, "global", False),  # head + 4097 words: uncached
+    (131712, 4608, 128, 512, 8, "v3", True),    # eight v3 segments of exactly 16384 scores
 ]
 
 
@@ -766,6 +778,162 @@ def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
         for layer in range(n_layers):
             for path in paths[1:]:
                 assert torch.equal(results["walk"][kind][layer], results[path][kind][layer])
+
+
+def _shared_kv_buffers(g, n_layers, pages, kv, dim, dtype, pad, device):
+    """Per layer one buffer [pages][K page | V page | pad elements], the
+    padding filled with NaN; returns (buffers, K views, V views)."""
+    page = 128 * kv * dim
+    stride = 2 * page + pad
+    shape, strides = (pages, 128, kv, dim), (stride, kv * dim, dim, 1)
+    bufs, ks, vs = [], [], []
+    for _ in range(n_layers):
+        buf = torch.full((pages * stride,), float("nan"), dtype=dtype)
+        k = torch.as_strided(buf, shape, strides, 0)
+        v = torch.as_strided(buf, shape, strides, page)
+        k.copy_(torch.randn(shape, generator=g))
+        v.copy_(torch.randn(shape, generator=g))
+        buf = buf.to(device)
+        bufs.append(buf)
+        ks.append(torch.as_strided(buf, shape, strides, 0))
+        vs.append(torch.as_strided(buf, shape, strides, page))
+    return bufs, ks, vs
+
+
+def _padding_bits(buf, pages, kv, dim, pad):
+    page = 128 * kv * dim
+    return buf.view(pages, 2 * page + pad)[:, 2 * page :].cpu().view(torch.int16)
+
+
+@pytest.mark.parametrize("path", ["walk", "plan", "plan-interleaved"])
+@pytest.mark.parametrize("mode", ["private", "inplace"])
+@pytest.mark.parametrize("pad", [0, 8, 4], ids=["pad0", "pad8", "pad4-8B-words"])
+def test_compact_shared_kv_buffer(hip_device, mode: str, path: str, pad: int) -> None:
+    """Every compaction form on K and V as interleaved views of one buffer per
+    layer with padded pages (tests/test_cache.py:50-94 at 128-token blocks;
+    pkg/provider.py:1201-1230): rows bit-exact against the reference's
+    materialisation and every padding element untouched.  Padding of 4
+    elements (the reference KAT's) moves the rows in 8-byte words."""
+    _, _, cache = _kvc()
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    g = torch.Generator().manual_seed(pad * 13 + len(mode) + len(path))
+    kv, dim, n_layers, budget = 4, 128, 3, 640
+    lens = [2000, 1500, 641]
+    pool = sum(-(-n // 128) for n in lens) + (0 if mode == "inplace" else 5 * len(lens)) + 3
+    perm = torch.randperm(pool, generator=g).tolist()
+    cur, src_tables, dst_tables = 0, [], []
+    for n in lens:
+        src_tables.append(perm[cur : cur + -(-n // 128)])
+        cur += -(-n // 128)
+    if mode == "private":
+        for _ in lens:
+            dst_tables.append(perm[cur : cur + 5])
+            cur += 5
+    keeps = [torch.sort(torch.randperm(n, generator=g)[:budget]).values for n in lens]
+    if mode == "inplace":
+        # One sequence whose hazard rows read rows the safe rows overwrite.
+        half = budget // 2
+        keeps[0] = torch.cat([2 * torch.arange(half) + 1, torch.arange(budget, 2 * budget - half)])
+    bufs, ks_d, vs_d = _shared_kv_buffers(g, n_layers, pool, kv, dim, torch.bfloat16, pad, hip_device)
+    ks = [k.cpu() for k in ks_d]
+    vs = [v.cpu() for v in vs_d]
+    pad_before = [_padding_bits(b, pool, kv, dim, pad) for b in bufs] if pad else None
+    for b, n in enumerate(lens):
+        dst = torch.tensor(dst_tables[b] if mode == "private" else src_tables[b][: -(-budget // 128)])
+        ref.method_compress(ks, vs, torch.tensor(src_tables[b]), dst, keeps[b], budget)
+    so, si, _ = dev.ragged(src_tables, hip_device)
+    do = di = None
+    if mode == "private":
+        do, di, _ = dev.ragged(dst_tables, hip_device)
+    cache.compact_layers(
+        dev.pointer_table(ks_d, hip_device),
+        dev.pointer_table(vs_d, hip_device),
+        num_pages=pool,
+        page_stride=int(ks_d[0].stride(0)),
+        row_elems=kv * dim,
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=hip_device),
+        src_block_offsets=so,
+        src_block_ids=si,
+        dst_block_offsets=do,
+        dst_block_ids=di,
+        keep=torch.stack(keeps).to(hip_device),
+        budget=budget,
+        workspace=None
+        if path == "walk"
+        else torch.empty(cache.compact_workspace_bytes(len(lens), budget), dtype=torch.uint8, device=hip_device),
+        layer_order="interleaved" if path == "plan-interleaved" else "layer_major",
+    )
+    torch.cuda.synchronize()
+    for layer in range(n_layers):
+        assert torch.equal(ks_d[layer].cpu(), ks[layer]), f"K layer {layer} differs"
+        assert torch.equal(vs_d[layer].cpu(), vs[layer]), f"V layer {layer} differs"
+        if pad:
+            assert torch.equal(_padding_bits(bufs[layer], pool, kv, dim, pad), pad_before[layer]), f"layer {layer} padding written"
+
+
+SHARED_SCORE_CASES = [
+    # (kv, qpk, head_dim, rotary, dtype, tokens, pad, aggregation)
+    (8, 5, 128, 128, torch.bfloat16, 1500, 8, "mean"),
+    (8, 5, 128, 128, torch.float16, 1300, 64, "mean"),
+    (2, 8, 256, 64, torch.bfloat16, 900, 0, "mean"),
+    (8, 5, 128, 128, torch.bfloat16, 1100, 8, "max"),
+    (2, 8, 256, 64, torch.float16, 700, 16, "max"),
+]
+
+
+@pytest.mark.parametrize("case", SHARED_SCORE_CASES, ids=[f"kv{c[0]}d{c[2]}r{c[3]}{str(c[4]).split('.')[-1]}pad{c[6]}-{c[7]}" for c in SHARED_SCORE_CASES])
+def test_score_paged_shared_kv_buffer(hip_device, case) -> None:
+    """Both scorers reading K as a view of a shared K/V buffer with padded
+    pages (the padding is NaN: a stray read would poison the scores), against
+    the oracle."""
+    kernels, _, _ = _kvc()
+    kv, qpk, head_dim, rotary, dtype, tokens, pad, aggregation = case
+    g = torch.Generator().manual_seed(tokens + pad)
+    stats = _random_stats(g, kv, qpk, rotary // 2, head_dim - rotary, rotary)
+    n_blocks = -(-tokens // 128)
+    pool = n_blocks + 4
+    _, ks_d, _ = _shared_kv_buffers(g, 1, pool, kv, head_dim, dtype, pad, hip_device)
+    k_d = ks_d[0]
+    blocks = torch.randperm(pool, generator=g)[:n_blocks]
+    max_len = 32768 if aggregation == "mean" else 131072
+    offsets = ref.build_geometric_offsets(max_len)
+    round_start = tokens + 9
+    keys = ref.gather_paged_range(k_d.cpu(), blocks, start=0, count=tokens, block_size=128)
+    want = ref.score_post_rope_keys(keys, stats, round_start=round_start, offsets=offsets, aggregation=aggregation)
+    out = torch.full((kv, qpk, tokens), float("nan"), device=hip_device)
+    d = lambda t: None if t is None else t.to(hip_device)  # noqa: E731
+    common = (d(stats.q_mean_real), d(stats.q_mean_imag), d(torch.sqrt(stats.freq_scale_sq)),
+              d(stats.q_abs_mean - torch.sqrt(stats.q_mean_real.square() + stats.q_mean_imag.square() + 1e-8)))
+    extra = dict(q_pass_mean=d(stats.q_pass_mean), rotary_dim=rotary if rotary != head_dim else None)
+    if aggregation == "mean":
+        cos, sin = kernels.mean_phase_table(
+            torch.tensor([round_start], dtype=torch.int64, device=hip_device), offsets.to(hip_device), stats.omega.view(1, -1).to(hip_device)
+        )
+        assert kernels.score_paged_keys_mean_precomputed(k_d, blocks.to(hip_device), *common, cos.view(-1), sin.view(-1),
+                                                         tokens, out, 128, "half", **extra)
+    else:
+        assert kernels.score_paged_keys_max(k_d, blocks.to(hip_device), *common, d(stats.omega), d(offsets), round_start,
+                                            tokens, out, 128, "half", **extra)
+    assert_scores_close(out.cpu().reshape(kv * qpk, tokens), want.reshape(kv * qpk, tokens))
+
+
+def test_score_rejects_pages_off_16_byte_boundaries(hip_device) -> None:
+    # A page stride padded by 4 bf16 elements puts odd pages 8 bytes off a
+    # 16-byte boundary: the scorers refuse it (the compaction moves such rows
+    # in 8-byte words, test_compact_shared_kv_buffer).
+    kernels, _, _ = _kvc()
+    g = torch.Generator().manual_seed(5)
+    stats = _random_stats(g, 2, 4, 64, 0, 128)
+    _, ks_d, _ = _shared_kv_buffers(g, 1, 4, 2, 128, torch.bfloat16, 4, hip_device)
+    out = torch.empty((2, 4, 256), device=hip_device)
+    d = lambda t: t.to(hip_device)  # noqa: E731
+    cos = torch.zeros(64, device=hip_device)
+    with pytest.raises(ValueError, match="16 bytes"):
+        kernels.score_paged_keys_mean_precomputed(
+            ks_d[0], torch.arange(2, device=hip_device), d(stats.q_mean_real), d(stats.q_mean_imag),
+            d(torch.sqrt(stats.freq_scale_sq)), d(stats.q_abs_mean), cos, cos, 256, out, 128, "half",
+        )
 
 
 def test_materialize_token_slots_padded_pages(hip_device) -> None:

@@ -86,14 +86,28 @@ def _run_and_check(spec, hip_device, *, check_layers=None, score_aggregation="me
             want_k = ref.gather_slots(host.k_caches[layer], slots)
             want_v = ref.gather_slots(host.v_caches[layer], slots)
             dslots = ref.token_slots(dst.to(hip_device), torch.arange(spec.budget, device=hip_device), 128)
-            got_k = cache.k_caches[layer].view(-1, spec.num_kv_heads, spec.head_dim)[dslots].cpu()
-            got_v = cache.v_caches[layer].view(-1, spec.num_kv_heads, spec.head_dim)[dslots].cpu()
+            got_k = ref.gather_slots(cache.k_caches[layer], dslots).cpu()
+            got_v = ref.gather_slots(cache.v_caches[layer], dslots).cpu()
             assert torch.equal(got_k, want_k), f"K layer {layer} seq {b}"
             assert torch.equal(got_v, want_v), f"V layer {layer} seq {b}"
         want_table, want_freed = ref.rewrite_block_table(src.tolist(), None if spec.inplace else dst.tolist(), spec.budget)
         assert tables[b].cpu().tolist() == want_table
         assert freed[b].cpu().tolist() == want_freed
+    if cache.kv_buffers is not None:
+        _assert_padding_untouched(cache)
     return pipeline, keep, oracle_keeps, near_ties
+
+
+def _assert_padding_untouched(cache) -> None:
+    """Every page's padding of the shared K/V buffers still holds its fill
+    (NaN, compared bit for bit)."""
+    from kvcompress_mi355x import workloads
+
+    num_pages = int(cache.k_caches[0].shape[0])
+    fill = torch.full((1,), workloads.PAD_VALUE, dtype=cache.spec.dtype).view(torch.int16)
+    for layer, buf in enumerate(cache.kv_buffers):
+        pad = workloads.padding_view(buf, num_pages, cache.spec)
+        assert torch.equal(pad.view(torch.int16).cpu(), fill.expand_as(pad)), f"layer {layer} padding was written"
 
 
 def test_config1_end_to_end(hip_device) -> None:
@@ -175,13 +189,48 @@ def test_fp16_decode_shape(hip_device) -> None:
     _run_and_check(spec, hip_device)
 
 
-def test_method_api_compress(hip_device, tmp_path) -> None:
-    """TriAttentionMethod through method API v1 on a bound synthetic cache."""
+SHARED_BUFFER_CASES = [
+    # (config, overrides, score aggregation); K and V interleaved in one buffer
+    # per layer, pages padded by page_pad elements (a multiple of 8: 16 bytes).
+    (2, dict(n_layers=4, score_layer_stride=2, seq_lens=(4224, 6000), budget=2048, max_model_len=16384, page_pad=0), "mean"),
+    (2, dict(n_layers=4, score_layer_stride=2, seq_lens=(4224, 6000), budget=2048, max_model_len=16384, page_pad=8), "mean"),
+    (5, dict(n_layers=2, score_layer_stride=1, seq_lens=(4300, 5000), page_pad=64), "mean"),
+    (3, dict(n_layers=4, seq_lens=(9000, 6000), page_pad=8), "mean"),
+    (4, dict(n_layers=2, score_layer_stride=1, seq_lens=(12000, 7000), pool_pages=200, max_model_len=32768, page_pad=8), "mean"),
+    (2, dict(n_layers=4, score_layer_stride=2, seq_lens=(5000, 4300), budget=2048, max_model_len=131072, page_pad=8), "max"),
+]
+
+
+@pytest.mark.parametrize(
+    "config, overrides, score_aggregation",
+    SHARED_BUFFER_CASES,
+    ids=["bf16-pad0", "bf16-pad8", "fp16-pad64", "qwen3.5-v3-pad8", "inplace-pad8", "max-o18-pad8"],
+)
+def test_shared_kv_buffer_layouts(hip_device, config, overrides, score_aggregation) -> None:
+    """The step on the reference's shared-buffer cache layout: K and V of a
+    layer are interleaved views of one buffer, each page followed by its
+    padding (tests/test_cache.py:50-94; pkg/provider.py:1201-1230).  Scores,
+    statistics, aggregate and keep set against the oracle, compaction bit-exact
+    in every layer, the padding untouched."""
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(config, kv_layout="interleaved", **overrides)
+    _, _, _, near = _run_and_check(spec, hip_device, score_aggregation=score_aggregation)
+    assert near <= 4
+
+
+@pytest.mark.parametrize("layout", [("separate", 0), ("interleaved", 0), ("interleaved", 24)], ids=["separate", "shared-kv", "shared-kv-pad24"])
+def test_method_api_compress(hip_device, tmp_path, layout) -> None:
+    """TriAttentionMethod through method API v1 on a bound synthetic cache:
+    one tensor per layer and kind, or K and V as interleaved views of one
+    (padded) buffer per layer as the reference's cache contract allows
+    (pkg/provider.py:1201-1230)."""
     from kvcompress_mi355x.methods import create_method
     from kvcompress_mi355x.methods.base import CompressionRequest, LayerCache
     from kvcompress_mi355x import workloads
 
-    spec = workloads.config_spec(2, n_layers=4, score_layer_stride=2, seq_lens=(6000,), budget=2048, recent=128, max_model_len=16384)
+    spec = workloads.config_spec(2, n_layers=4, score_layer_stride=2, seq_lens=(6000,), budget=2048, recent=128,
+                                 max_model_len=16384, kv_layout=layout[0], page_pad=layout[1])
     host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
     cache = workloads.move_cache(host, hip_device)
     stats_path = tmp_path / "stats.pt"
@@ -236,7 +285,10 @@ def test_method_api_compress(hip_device, tmp_path) -> None:
     slots = ref.token_slots(src.cpu(), keep_only.cpu(), 128)
     dslots = ref.token_slots(dst, torch.arange(2048, device=hip_device), 128)
     for i in range(spec.n_layers):
-        assert torch.equal(cache.k_caches[i].view(-1, 8, 128)[dslots].cpu(), ref.gather_slots(host.k_caches[i], slots))
+        assert torch.equal(ref.gather_slots(cache.k_caches[i], dslots).cpu(), ref.gather_slots(host.k_caches[i], slots))
+        assert torch.equal(ref.gather_slots(cache.v_caches[i], dslots).cpu(), ref.gather_slots(host.v_caches[i], slots))
+    if cache.kv_buffers is not None:
+        _assert_padding_untouched(cache)
 
 
 def test_pipeline_reused_with_a_smaller_batch(hip_device) -> None:

@@ -261,6 +261,85 @@ def test_cache_validation_matches_reference_contract() -> None:
         dev.validate_cache(torch.zeros(2, 128, 1, 8), "k")  # host tensor
 
 
+@pytest.mark.parametrize("pad, accepted", [(0, True), (8, True), (64, True), (4, False), (2, False), (12, False)])
+def test_page_stride_must_keep_16_byte_pages(pad: int, accepted: bool) -> None:
+    """The scorers read 16-byte words: K/V views of a shared buffer pass when
+    the per-page padding is a multiple of 8 bf16 elements and are refused
+    with a clear error otherwise (the reference accepts any stride of at least
+    one page, pkg/provider.py:1224-1230; tests/test_cache.py:50-94 pads 4)."""
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    kv, dim, pages = 2, 64, 3
+    page = 128 * kv * dim
+    stride = 2 * page + pad
+    raw = torch.zeros(pages * stride + 64, dtype=torch.bfloat16)
+    offset = (-raw.data_ptr() // 2) % 8  # a 16-byte aligned start inside the allocation
+    shape, strides = (pages, 128, kv, dim), (stride, kv * dim, dim, 1)
+    k = torch.as_strided(raw, shape, strides, offset)
+    v = torch.as_strided(raw, shape, strides, offset + page)
+    for view in (k, v):
+        if accepted:
+            dev.require_16_byte_pages(view, "k_cache")
+        else:
+            with pytest.raises(ValueError, match="multiples of 16 bytes"):
+                dev.require_16_byte_pages(view, "k_cache")
+    misaligned = torch.as_strided(raw, shape, (2 * page, kv * dim, dim, 1), offset + 1)
+    with pytest.raises(ValueError, match="16 bytes"):
+        dev.require_16_byte_pages(misaligned, "k_cache")
+
+
+class _FakeTensor:
+    def __init__(self, key):
+        self.key = key
+        self.device = "dev0"
+        self.recorded = []
+
+    def record_stream(self, stream):
+        self.recorded.append(stream)
+
+
+def test_descriptor_cache_pins_captured_entries_and_records_streams() -> None:
+    """One-sequence descriptors: least-recently-used eviction outside graph
+    capture, entries made or used during capture never evicted, and a
+    descriptor used on another stream than its allocation's recorded there."""
+    from kvcompress_mi355x.methods.triattention._device import DescriptorCache
+
+    state = {"capturing": False, "stream": "s0"}
+    made = []
+
+    def make(key):
+        made.append(key)
+        return _FakeTensor(key)
+
+    cache = DescriptorCache(maxsize=2, make=make, capturing=lambda: state["capturing"],
+                            current_stream=lambda device: state["stream"])
+    a = cache.get(("a",))
+    assert cache.get(("a",)) is a and made == [("a",)]
+    state["capturing"] = True
+    cap = cache.get(("captured",))
+    assert cache.pinned(("captured",))
+    state["capturing"] = False
+    for i in range(10):
+        cache.get((i,))
+    assert cache.get(("captured",)) is cap  # never evicted
+    assert made.count(("captured",)) == 1
+    assert cache.get(("a",)) is not a  # evicted and made again
+    # An entry used (not made) during capture is pinned too.
+    state["capturing"] = True
+    cache.get((9,))
+    state["capturing"] = False
+    for i in range(20, 30):
+        cache.get((i,))
+    assert cache.pinned((9,)) and made.count((9,)) == 1
+    # Use on another stream records the descriptor there.
+    state["stream"] = "s1"
+    t = cache.get(("captured",))
+    assert t.recorded == ["s1"]
+    state["stream"] = "s0"
+    cache.get(("captured",))
+    assert t.recorded == ["s1"]
+
+
 # ------------------------------------------------------------------ C ABI --
 
 

@@ -96,6 +96,49 @@ def test_noalloc_scorer_matches_workspace_scorer_twice(hip_device, config):
     _check_call(pipeline, small)
 
 
+@pytest.mark.gpu
+def test_noalloc_scorer_under_graph_capture(hip_device):
+    """The entry point captured into a HIP graph on a side stream (after one
+    eager call on the device, which takes the scratch array's address):
+    two replays, each after the outputs are overwritten with NaN by eager
+    work, give the workspace path's raw scores and statistics bit for bit."""
+    spec = workloads.config_spec(2, n_layers=16, seq_lens=(16384, 9000))
+    cache = workloads.build_synthetic_cache(spec, hip_device, seed=4)
+    pipeline, batch = workloads.build_pipeline(cache)
+    pipeline.score(batch)
+    total = batch.total_tokens
+    want_raw = pipeline.raw_scores()[:, :total].clone()
+    want_mean, want_var = (t.clone() for t in pipeline.head_statistics(batch))
+    s, h = pipeline.tables.n_layers, pipeline.n_heads
+    raw2 = torch.full_like(pipeline.raw, float("nan"))
+    mean2 = torch.full((s, batch.n_seq, h), float("nan"), device=pipeline.device)
+    var2 = torch.full_like(mean2, float("nan"))
+
+    def check() -> None:
+        got_raw = raw2.transpose(1, 2) if pipeline.head_major else raw2
+        assert torch.equal(got_raw[:, :total], want_raw)
+        assert torch.equal(mean2, want_mean)
+        assert torch.equal(var2, want_var)
+
+    assert _noalloc(pipeline, batch, raw2, mean2, var2) == 0, _native.load().kvc_last_error().decode()
+    torch.cuda.synchronize()
+    check()
+    side = torch.cuda.Stream(device=pipeline.device)
+    side.wait_stream(torch.cuda.current_stream(pipeline.device))
+    graph = torch.cuda.CUDAGraph()
+    codes = []
+    with torch.cuda.graph(graph, stream=side):
+        codes.append(_noalloc(pipeline, batch, raw2, mean2, var2))
+    assert codes == [0], _native.load().kvc_last_error().decode()
+    for _ in range(2):
+        for t in (raw2, mean2, var2):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check()
+
+
 def test_noalloc_scorer_rejects_batches_beyond_its_scratch():
     lib = _native.load()
     # 6 scoring layers x 64 sequences of 131072 tokens x 40 query heads: the

@@ -31,9 +31,12 @@ tools read or write the same files: the CalibrationRequest fields, the
 command-line flags, the schema-3 layout and metadata keys, and the
 model-source fingerprint ("identifier:" + SHA-256 of "<model>@<revision>", or
 "local-manifest:" + SHA-256 of the checkpoint directory's file manifest), so an
-artifact validates on either side.  Artifacts carry this build's generator
-name; the model-source provenance check applies to artifacts of this
-generator and of the reference's.  The built-in calibration text is this
+artifact validates on either side.  Artifacts name the reference's
+generator ("generator": "vllm-ascend-kvcompress-hust"), because the
+reference's loader holds an artifact to its recorded model source only under
+that name (pkg/calibration.py:426-452); this package is recorded under
+"producer" / "producer_version".  The model-source provenance check here
+applies to either generator name.  The built-in calibration text is this
 package's own (input_source "builtin:mi355x-systems-v1").
 """
 
@@ -62,6 +65,8 @@ from .methods.triattention.config import TriAttentionConfig
 from .methods.triattention.stats import SUPPORTED_MODEL_TYPES, CalibrationStats
 from .model import model_shape_from_config
 
+# The software that wrote an artifact ("producer") and the generator name its
+# metadata carries: the reference's, so that its loader checks provenance.
 GENERATOR = "kvcompress-mi355x"
 REFERENCE_GENERATOR = "vllm-ascend-kvcompress-hust"
 # Generators whose artifacts record the model source they were made from.
@@ -645,8 +650,9 @@ def _artifact(request: CalibrationRequest) -> dict[str, Any]:
     metadata = {
         # provenance
         "schema_version": SCHEMA_VERSION,
-        "generator": GENERATOR,
-        "generator_version": __version__,
+        "generator": REFERENCE_GENERATOR,
+        "producer": GENERATOR,
+        "producer_version": __version__,
         "accumulator": "kvc_qstats_accumulate (float64 sums, HIP)",
         "transformers_version": checkpoint.transformers.__version__,
         "created_at_utc": datetime.now(timezone.utc).isoformat(),

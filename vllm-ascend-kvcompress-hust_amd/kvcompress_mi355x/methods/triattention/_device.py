@@ -2,7 +2,7 @@
 
 from __future__ import annotations
 
-import functools
+from collections import OrderedDict
 
 import torch
 
@@ -65,6 +65,20 @@ def validate_cache(cache: torch.Tensor, name: str, block_size: int = 128) -> Non
         raise ValueError(f"{name} must have contiguous inner blocks and a non-overlapping page stride")
 
 
+def require_16_byte_pages(cache: torch.Tensor, name: str) -> None:
+    """The scorers read keys in 16-byte words, so every page must start on a
+    16-byte boundary: the base address and the page stride in bytes must be
+    multiples of 16.  The reference accepts any page stride of at least one
+    page (pkg/provider.py:1224-1230); a stride padded by a multiple of 8
+    elements (bf16/fp16), e.g. K and V interleaved in one [pages, 2, ...]
+    buffer, passes; an odd padding such as 4 elements does not."""
+    if cache.data_ptr() % 16 or (cache.stride(0) * cache.element_size()) % 16:
+        raise ValueError(
+            f"{name}: the HIP scorer reads 16-byte words; the cache base address and its page stride "
+            f"({cache.stride(0)} elements) must be multiples of 16 bytes"
+        )
+
+
 def pointer_table(tensors: list[torch.Tensor], device: torch.device) -> torch.Tensor:
     """Device array of base addresses (uint64 stored in int64)."""
     values = [int(t.data_ptr()) for t in tensors]
@@ -88,19 +102,71 @@ def ragged(rows: list[torch.Tensor | list[int] | tuple[int, ...]], device: torch
     return torch.tensor(offsets, dtype=torch.int64, device=device), flat.contiguous(), lengths
 
 
-@functools.lru_cache(maxsize=256)
-def _one_sequence_descriptor(device_index: int, layer_ptr: int, num_tokens: int, n_blocks: int) -> torch.Tensor:
+class DescriptorCache:
+    """Device descriptors of one-sequence launches, one per distinct value.
+
+    A descriptor is a small device tensor whose address goes into kernel
+    launches; it must outlive every launch that reads it.  Entries made or
+    used while the current stream is capturing a graph are pinned for the
+    life of the cache (a replay reads the captured address at any later
+    time); the others are kept least-recently-used, ``maxsize`` of them.  A
+    descriptor used on a stream other than the one it was allocated on is
+    recorded on that stream, so that evicting it cannot hand its memory to a
+    new allocation while a kernel queued there still reads it.  ``make``,
+    ``capturing`` and ``stream_of`` are injectable for host-only tests."""
+
+    def __init__(self, maxsize: int = 256, *, make=None, capturing=None, current_stream=None) -> None:
+        self.maxsize = int(maxsize)
+        self._lru: OrderedDict = OrderedDict()
+        self._pinned: dict = {}
+        self._make = make or _make_descriptor
+        self._capturing = capturing or torch.cuda.is_current_stream_capturing
+        self._current_stream = current_stream or (lambda device: torch.cuda.current_stream(device))
+
+    def __len__(self) -> int:
+        return len(self._lru) + len(self._pinned)
+
+    def pinned(self, key) -> bool:
+        return key in self._pinned
+
+    def get(self, key: tuple) -> torch.Tensor:
+        entry = self._pinned.get(key)
+        if entry is None:
+            entry = self._lru.pop(key, None)
+            if entry is None:
+                tensor = self._make(key)
+                entry = (tensor, self._current_stream(tensor.device))
+            if self._capturing():
+                self._pinned[key] = entry
+            else:
+                self._lru[key] = entry
+                while len(self._lru) > self.maxsize:
+                    self._lru.popitem(last=False)
+        tensor, made_on = entry
+        stream = self._current_stream(tensor.device)
+        if stream != made_on:
+            tensor.record_stream(stream)
+        return tensor
+
+
+def _make_descriptor(key: tuple) -> torch.Tensor:
+    device_index, layer_ptr, num_tokens, n_blocks = key
     signed = layer_ptr - (1 << 64) if layer_ptr >= (1 << 63) else layer_ptr
     # int64 words: [layer pointer, token offsets (0, n), block offsets (0, blocks), sequence length in the low half]
     return torch.tensor([signed, 0, num_tokens, 0, n_blocks, num_tokens], dtype=torch.int64,
                         device=torch.device("cuda", device_index))
 
 
-def one_sequence_descriptor(layer: torch.Tensor, num_tokens: int, n_blocks: int) -> dict[str, int]:
+_DESCRIPTORS = DescriptorCache()
+
+
+def one_sequence_descriptor(layer: torch.Tensor, num_tokens: int, n_blocks: int) -> dict:
     """Device addresses of the batch descriptor of a one-layer, one-sequence
     launch (layer pointer table, token and block offsets, int32 sequence
     length), kept on the device per distinct value so that repeated calls
-    copy nothing to the device.  The words are immutable once made."""
-    t = _one_sequence_descriptor(layer.device.index, int(layer.data_ptr()), int(num_tokens), int(n_blocks))
+    copy nothing to the device; ``"tensor"`` is the descriptor itself, for
+    callers that hold on to their launch arguments.  The words are immutable
+    once made."""
+    t = _DESCRIPTORS.get((layer.device.index, int(layer.data_ptr()), int(num_tokens), int(n_blocks)))
     base = int(t.data_ptr())
-    return {"layer_ptrs": base, "token_offsets": base + 8, "block_offsets": base + 24, "seq_lens": base + 40}
+    return {"tensor": t, "layer_ptrs": base, "token_offsets": base + 8, "block_offsets": base + 24, "seq_lens": base + 40}

@@ -115,8 +115,7 @@ def _single_layer_scoring(
         raise ValueError("full-RoPE scoring must not pass q_pass_mean")
     if int(k_cache.shape[2]) != kv_heads:
         raise ValueError("calibration KV-head count does not match cache keys")
-    if k_cache.stride(0) % 8 or k_cache.data_ptr() % 16:
-        raise ValueError("the HIP scorer reads 16-byte words: page stride must be a multiple of 8 elements")
+    dev.require_16_byte_pages(k_cache, "k_cache")
     for name, t in (
         ("q_real", q_real),
         ("q_imag", q_imag),

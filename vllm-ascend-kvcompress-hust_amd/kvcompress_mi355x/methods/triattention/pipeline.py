@@ -189,8 +189,7 @@ class CompressionPipeline:
             dev.validate_cache(cache, f"cache[{i}]")
             if cache.shape != reference.shape or cache.stride() != reference.stride() or cache.dtype != reference.dtype:
                 raise ValueError("every cache layer must share shape, strides and dtype")
-            if cache.data_ptr() % 16 or cache.stride(0) % 8:
-                raise ValueError("cache base addresses and page strides must be 16-byte aligned")
+            dev.require_16_byte_pages(cache, f"cache[{i}]")
         if layer_aggregation not in ("mean", "max"):
             raise ValueError(f"unsupported layer aggregation {layer_aggregation!r}")
         if score_aggregation not in ("mean", "max"):

@@ -45,6 +45,12 @@ class WorkloadSpec:
     permute_pages: bool = True
     pool_pages: int | None = None
     model_type: str = "qwen2"
+    # "separate": one [pages, 128, kv, D] tensor per layer and K/V;
+    # "interleaved": K and V of a layer are views of one buffer whose page i
+    # holds K's page, then V's page, then `page_pad` elements of padding (the
+    # shared-buffer layout of pkg/provider.py:1201-1230, tests/test_cache.py:50-94).
+    kv_layout: str = "separate"
+    page_pad: int = 0
     notes: tuple[str, ...] = field(default_factory=tuple)
 
     @property
@@ -209,10 +215,32 @@ class SyntheticCache:
     destination_tables: list[torch.Tensor] | None
     calibration: CalibrationStats
     round_starts: list[int]
+    kv_buffers: list[torch.Tensor] | None = None  # the interleaved layout's per-layer buffers
 
     @property
     def seq_lens(self) -> list[int]:
         return list(self.spec.seq_lens)
+
+
+# Padding elements of the interleaved layout hold this value (NaN) so that a
+# kernel reading them shows up in its results; compaction must leave them alone.
+PAD_VALUE = float("nan")
+
+
+def interleaved_views(buffer: torch.Tensor, num_pages: int, spec: WorkloadSpec) -> tuple[torch.Tensor, torch.Tensor]:
+    """K and V [pages, 128, kv, D] views of one layer's interleaved buffer."""
+    row = spec.num_kv_heads * spec.head_dim
+    page = KERNEL_BLOCK_SIZE * row
+    stride = 2 * page + spec.page_pad
+    shape = (num_pages, KERNEL_BLOCK_SIZE, spec.num_kv_heads, spec.head_dim)
+    strides = (stride, row, spec.head_dim, 1)
+    return torch.as_strided(buffer, shape, strides, 0), torch.as_strided(buffer, shape, strides, page)
+
+
+def padding_view(buffer: torch.Tensor, num_pages: int, spec: WorkloadSpec) -> torch.Tensor:
+    """[pages, page_pad] view of the padding of an interleaved buffer."""
+    page = KERNEL_BLOCK_SIZE * spec.num_kv_heads * spec.head_dim
+    return buffer.view(num_pages, 2 * page + spec.page_pad)[:, 2 * page :]
 
 
 def synthetic_calibration(spec: WorkloadSpec, seed: int = 1) -> CalibrationStats:
@@ -309,19 +337,38 @@ def build_synthetic_cache(
         outlier_rows = outlier_rows.to(device)
     cg = torch.Generator().manual_seed(seed + 7)
     pool = None
+    kv_buffers = None
+    if spec.kv_layout not in ("separate", "interleaved"):
+        raise ValueError(f"unknown KV layout {spec.kv_layout!r}")
+    if spec.kv_layout == "interleaved":
+        if arena:
+            raise ValueError("the interleaved KV layout has one buffer per layer; it has no arena form")
+        page = KERNEL_BLOCK_SIZE * spec.num_kv_heads * spec.head_dim
+        kv_buffers = [
+            torch.full((num_pages * (2 * page + spec.page_pad),), PAD_VALUE, dtype=spec.dtype, device=device)
+            for _ in range(spec.n_layers)
+        ]
+        if used_index is not None:
+            for buf in kv_buffers:
+                k_view, v_view = interleaved_views(buf, num_pages, spec)
+                k_view.zero_()
+                v_view.zero_()
+    elif spec.page_pad:
+        raise ValueError("page padding applies to the interleaved KV layout")
     if arena:
         alloc = torch.empty if used_index is None else torch.zeros
         pool = alloc((2 * spec.n_layers * num_pages,) + shape[1:], dtype=spec.dtype, device=device)
     for layer in range(spec.n_layers):
         caches = []
         for kind in range(2):
-            if pool is not None:
+            if kv_buffers is not None:
+                cache = interleaved_views(kv_buffers[layer], num_pages, spec)[kind]
+            elif pool is not None:
                 start = (2 * layer + kind) * num_pages
                 cache = pool[start : start + num_pages]
             else:
                 cache = (torch.empty if used_index is None else torch.zeros)(shape, dtype=spec.dtype, device=device)
-            flat = cache.view(num_pages, -1)
-            step = max(1, (1 << 26) // flat.shape[1])  # fill in bounded float32 chunks
+            step = max(1, (1 << 26) // (KERNEL_BLOCK_SIZE * spec.num_kv_heads * spec.head_dim))  # bounded float32 chunks
             scale = None
             if spec.channel_scale_sigma > 0:
                 scale = (1.0 + spec.channel_scale_sigma * torch.randn(spec.num_kv_heads, spec.head_dim, generator=cg)).to(device)
@@ -335,8 +382,9 @@ def build_synthetic_cache(
                 else:
                     cache.index_copy_(0, used_index[start:stop], chunk.to(spec.dtype))
             if outlier_rows is not None:
-                rows = cache.view(-1, spec.num_kv_heads, spec.head_dim)
-                rows[outlier_rows] = (rows[outlier_rows].float() * spec.outlier_scale).to(spec.dtype)
+                pages = outlier_rows // KERNEL_BLOCK_SIZE
+                offs = outlier_rows % KERNEL_BLOCK_SIZE
+                cache[pages, offs] = (cache[pages, offs].float() * spec.outlier_scale).to(spec.dtype)
             caches.append(cache)
         k_caches.append(caches[0])
         v_caches.append(caches[1])
@@ -349,20 +397,31 @@ def build_synthetic_cache(
         destination_tables=None if dst_tables is None else to_dev(dst_tables),
         calibration=synthetic_calibration(spec, seed + 1),
         round_starts=list(spec.seq_lens),
+        kv_buffers=kv_buffers,
     )
 
 
 def move_cache(cache: SyntheticCache, device: torch.device | str) -> SyntheticCache:
     """Copy a cache built on one device (e.g. the CPU, for oracle checks) to another."""
     to = lambda ts: [t.to(device) for t in ts]  # noqa: E731
+    kv_buffers = None
+    if cache.kv_buffers is not None:
+        # Views keep their layout only if the buffers move and the views are rebuilt.
+        kv_buffers = to(cache.kv_buffers)
+        num_pages = int(cache.k_caches[0].shape[0])
+        views = [interleaved_views(buf, num_pages, cache.spec) for buf in kv_buffers]
+        k_caches, v_caches = [k for k, _ in views], [v for _, v in views]
+    else:
+        k_caches, v_caches = to(cache.k_caches), to(cache.v_caches)
     return SyntheticCache(
         spec=cache.spec,
-        k_caches=to(cache.k_caches),
-        v_caches=to(cache.v_caches),
+        k_caches=k_caches,
+        v_caches=v_caches,
         source_tables=to(cache.source_tables),
         destination_tables=None if cache.destination_tables is None else to(cache.destination_tables),
         calibration=cache.calibration,
         round_starts=list(cache.round_starts),
+        kv_buffers=kv_buffers,
     )
 
 
