@@ -363,8 +363,10 @@ def aggregate_normalized_scores(
     device = scores.device
     m = mean.reshape(-1).contiguous()
     v = variance.reshape(-1).contiguous()
-    seq_lens = torch.tensor([num_tokens], dtype=torch.int32, device=device)
-    token_offsets = torch.tensor([0, num_tokens], dtype=torch.int64, device=device)
+    # One-sequence descriptor words (token offsets, sequence length), kept on
+    # the device per value: nothing is copied to the device per call, so the
+    # call can be captured into a graph.
+    desc = dev.one_sequence_descriptor(aggregate, num_tokens, 0)
     flags = _native.AGG_RSQRT | (0 if first_layer else _native.AGG_ACCUMULATE)
     _native.call(
         "kvc_aggregate",
@@ -373,8 +375,8 @@ def aggregate_normalized_scores(
         heads,
         1,
         num_tokens,
-        dev.ptr(seq_lens),
-        dev.ptr(token_offsets),
+        desc["seq_lens"],
+        desc["token_offsets"],
         dev.ptr(flat_scores),
         0,
         1,
