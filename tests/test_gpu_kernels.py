@@ -626,7 +626,7 @@ def _layers(g, n_layers, pages, kv, dim, dtype):
 
 @pytest.mark.parametrize("path", ["walk", "plan", "plan-interleaved"])
 @pytest.mark.parametrize("mode", ["private", "inplace"])
-@pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided", "split"])
+@pytest.mark.parametrize("pattern", ["random", "front", "tail", "strided", "split", "shift"])
 def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> None:
     """Every form (rows resolved per workgroup and every layer walked, or rows
     planned once into the workspace and moved one layer per workgroup, layer
@@ -663,6 +663,11 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> No
             k = torch.cat([2 * torch.arange(half) + 1, torch.arange(budget, 2 * budget - half)])
         elif pattern == "tail":
             k = torch.arange(n - budget, n)
+        elif pattern == "shift":
+            # In place, every row but the last is a hazard row reading the row
+            # after it, which the next row overwrites: a chain through three
+            # walk tiles of 256 rows.
+            k = torch.arange(1, budget + 1)
         else:
             k = torch.linspace(0, n - 1, budget).round().long().unique()
             while k.numel() < budget:

@@ -501,13 +501,15 @@ def test_compaction_form_schedule_and_margin():
     choice, forms = _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [4.30, 4.25]})
     assert forms[:6] == [("layer_major", False), ("interleaved", False), ("layer_major", True), ("interleaved", True),
                          ("layer_major", True), ("interleaved", True)]
-    assert choice.chosen == "interleaved"  # 4.25 < 0.97 * 4.45
+    assert choice.chosen == "interleaved"  # 4.25 < 0.99 * 4.45
     assert forms[6:] == [("interleaved", False), ("interleaved", False)]
     assert choice.per_row_ms == {"layer_major": 4.45 / 100, "interleaved": 4.25 / 100}
 
 
 def test_compaction_form_keeps_planned_inside_margin_and_when_slower():
-    assert _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [4.36, 4.40]})[0].chosen == "layer_major"
+    assert _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [4.42, 4.43]})[0].chosen == "layer_major"
+    # 1.6% faster (a placement seen on the Qwen2.5-14B pool) is past the margin.
+    assert _drive_choice({"layer_major": [4.38, 4.40], "interleaved": [4.31, 4.32]})[0].chosen == "interleaved"
     assert _drive_choice({"layer_major": [4.45, 4.46], "interleaved": [5.07, 5.08]})[0].chosen == "layer_major"
     # A slow first timed trial does not decide: the faster of each form's two counts.
     assert _drive_choice({"layer_major": [6.0, 4.45], "interleaved": [4.25, 7.0]})[0].chosen == "interleaved"
