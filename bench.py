@@ -82,6 +82,12 @@ def parse_args() -> argparse.Namespace:
         default="mean",
         help="aggregation of the rotary score over the future offsets (the reference's score_aggregation option)",
     )
+    p.add_argument(
+        "--compaction-order",
+        choices=("auto", "layer_major", "interleaved"),
+        default="auto",
+        help="compaction layer order: auto (time both on the cache, keep the faster) or a fixed one",
+    )
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument(
         "--cpu-repeats",
@@ -738,7 +744,8 @@ def measure(spec, args) -> dict:
 
     device = torch.device("cuda:0")
     cache = workloads.build_synthetic_cache(spec, device, seed=0, arena=args.arena)
-    pipeline, batch = workloads.build_pipeline(cache, score_aggregation=args.score_aggregation)
+    pipeline, batch = workloads.build_pipeline(cache, score_aggregation=args.score_aggregation,
+                                               compaction_order=getattr(args, "compaction_order", "auto"))
     restore = FrontRestore(cache, spec.budget) if args.restore_front else None
     # Pipeline set-up, untimed: the compaction form for this cache's
     # placement in HBM is chosen from timed trials of both forms.
@@ -841,6 +848,7 @@ def main() -> int:
             "compaction": "in-place" if spec.inplace else "private destinations",
             "kv_pool": m["kv_pool"],
             "compaction_form": m["compaction_form"],
+            **({"compaction_order": args.compaction_order} if args.compaction_order != "auto" else {}),
             "launch": "one HIP graph per step" if args.graph else "kernel launches per step",
             **({"score_aggregation": "max"} if args.score_aggregation == "max" else {}),
             **(

@@ -515,6 +515,22 @@ def test_compaction_form_keeps_planned_inside_margin_and_when_slower():
     assert _drive_choice({"layer_major": [6.0, 4.45], "interleaved": [4.25, 7.0]})[0].chosen == "interleaved"
 
 
+def test_compaction_form_fixed_order_skips_trials(monkeypatch):
+    from kvcompress_mi355x.methods.triattention.pipeline import CompactionFormChoice
+
+    choice = CompactionFormChoice(event_factory=lambda: None, capturing=lambda: False, fixed="interleaved")
+    assert [choice.next_call() for _ in range(3)] == [("interleaved", None)] * 3
+    with pytest.raises(ValueError, match="unknown compaction layer order"):
+        CompactionFormChoice(fixed="sideways")
+    monkeypatch.delenv(tri_method.COMPACTION_ORDER_ENV, raising=False)
+    assert tri_method.compaction_order_setting() == "auto"
+    monkeypatch.setenv(tri_method.COMPACTION_ORDER_ENV, "layer_major")
+    assert tri_method.compaction_order_setting() == "layer_major"
+    monkeypatch.setenv(tri_method.COMPACTION_ORDER_ENV, "fastest")
+    with pytest.raises(ValueError, match="must be one of auto, layer_major, interleaved"):
+        tri_method.compaction_order_setting()
+
+
 def test_compaction_form_waits_for_events_and_capture():
     from kvcompress_mi355x.methods.triattention.pipeline import CompactionFormChoice
 

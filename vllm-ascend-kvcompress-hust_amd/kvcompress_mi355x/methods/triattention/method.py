@@ -15,6 +15,7 @@ kernel for the whole batch); ``compress`` is the one-request case of it.
 
 from __future__ import annotations
 
+import os
 from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
 from typing import Any
@@ -32,7 +33,7 @@ from ..base import (
 )
 from . import _device as dev
 from .config import TriAttentionConfig
-from .pipeline import Batch, CompressionPipeline, ScoringTables, max_all_reducer
+from .pipeline import COMPACTION_ORDERS, Batch, CompressionPipeline, ScoringTables, max_all_reducer
 from .scoring import build_geometric_offsets
 from .stats import CalibrationStats, DeviceLayerCalibrationStats
 
@@ -44,6 +45,21 @@ def queries_per_kv_head(model_shape: ModelShape) -> int:
     if model_shape.num_attention_heads % model_shape.num_kv_heads:
         raise RuntimeError("TriAttention requires query heads divisible by KV heads")
     return model_shape.num_attention_heads // model_shape.num_kv_heads
+
+
+COMPACTION_ORDER_ENV = "KVCOMPRESS_MI355X_COMPACTION_ORDER"
+
+
+def compaction_order_setting() -> str:
+    """The compaction layer order a bound cache uses: the environment's
+    KVCOMPRESS_MI355X_COMPACTION_ORDER ("layer_major" or "interleaved" pins
+    it), else "auto", which times both orders on the cache's first
+    compactions and keeps the faster.  The method options stay the
+    reference's, so this deployment setting is not one of them."""
+    value = os.environ.get(COMPACTION_ORDER_ENV, "auto").strip() or "auto"
+    if value not in COMPACTION_ORDERS:
+        raise ValueError(f"{COMPACTION_ORDER_ENV} must be one of {', '.join(COMPACTION_ORDERS)}, got {value!r}")
+    return value
 
 
 def is_mtp_cache_layer(layer_name: str) -> bool:
@@ -174,6 +190,7 @@ class TriAttentionMethod(KVCompressionMethod):
             max_seqs=1,
             max_seq_len=max_len,
             score_aggregation=self.config.score_aggregation,
+            compaction_order=compaction_order_setting(),
         )
 
     # ------------------------------------------------------------ compress --

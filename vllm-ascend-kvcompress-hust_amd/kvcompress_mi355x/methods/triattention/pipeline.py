@@ -179,6 +179,7 @@ class CompressionPipeline:
         max_seq_len: int,
         max_tokens: int | None = None,
         score_aggregation: str = "mean",
+        compaction_order: str = "auto",
     ) -> None:
         if not scoring_k_caches or len(scoring_k_caches) != tables.n_layers:
             raise ValueError("one scoring K cache per scoring layer is required")
@@ -224,7 +225,9 @@ class CompressionPipeline:
         self.k_ptrs = dev.pointer_table(k_caches, self.device)
         self.v_ptrs = dev.pointer_table(v_caches, self.device)
         self._caches = (scoring_k_caches, k_caches, v_caches)  # keep the bound storage alive
-        self.compaction_form = CompactionFormChoice()
+        if compaction_order not in COMPACTION_ORDERS:
+            raise ValueError(f"compaction_order must be one of {', '.join(COMPACTION_ORDERS)}, got {compaction_order!r}")
+        self.compaction_form = CompactionFormChoice(fixed=None if compaction_order == "auto" else compaction_order)
         self._allocate(max_seqs, max_seq_len, max_tokens or max_seqs * max_seq_len)
 
     # ------------------------------------------------------------ buffers --
@@ -618,6 +621,10 @@ class CompressionPipeline:
         return StepGraph(graph, *outputs)
 
 
+# "auto": time both layer orders on the cache and keep the faster (CompactionFormChoice).
+COMPACTION_ORDERS = ("auto", "layer_major", "interleaved")
+
+
 class CompactionFormChoice:
     """Which layer order a pipeline's planned compaction uses for its cache.
 
@@ -634,7 +641,8 @@ class CompactionFormChoice:
     faster than the layer-major order's (repeated trials of one order differ
     by 0.2 - 0.5%), else the layer-major order.  Until
     then, and under graph capture, the layer-major order runs outside the
-    trial schedule.
+    trial schedule.  A ``fixed`` order is used from the first call, with no
+    trials.
     """
 
     FORMS = ("layer_major", "interleaved")
@@ -642,8 +650,10 @@ class CompactionFormChoice:
                 ("layer_major", True), ("interleaved", True))
     MARGIN = 0.99
 
-    def __init__(self, event_factory=None, capturing=None) -> None:
-        self.chosen: str | None = None
+    def __init__(self, event_factory=None, capturing=None, fixed: str | None = None) -> None:
+        if fixed is not None and fixed not in self.FORMS:
+            raise ValueError(f"unknown compaction layer order {fixed!r}")
+        self.chosen: str | None = fixed
         self.per_row_ms: dict[str, float] | None = None
         self._next = 0
         self._trials: list[tuple[str, tuple, int]] = []

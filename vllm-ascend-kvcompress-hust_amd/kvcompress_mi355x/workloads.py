@@ -425,7 +425,8 @@ def move_cache(cache: SyntheticCache, device: torch.device | str) -> SyntheticCa
     )
 
 
-def build_pipeline(cache: SyntheticCache, *, score_aggregation: str = "mean", layer_aggregation: str = "mean"):
+def build_pipeline(cache: SyntheticCache, *, score_aggregation: str = "mean", layer_aggregation: str = "mean",
+                   compaction_order: str = "auto"):
     """CompressionPipeline + Batch over a synthetic cache (all sequences)."""
     from .methods.triattention.pipeline import Batch, CompressionPipeline, ScoringTables
     from .methods.triattention.scoring import build_geometric_offsets
@@ -451,6 +452,7 @@ def build_pipeline(cache: SyntheticCache, *, score_aggregation: str = "mean", la
         max_seq_len=max(spec.seq_lens),
         max_tokens=spec.total_tokens,
         score_aggregation=score_aggregation,
+        compaction_order=compaction_order,
     )
     batch = Batch.build(
         device,
