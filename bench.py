@@ -544,9 +544,9 @@ def kernel_micro_bench(steps: int, warmup: int, cpu_repeats: int, no_cpu: bool) 
 
 def cpu_threads() -> tuple[int, dict]:
     """Host threads for a CPU baseline and how they were chosen: every core
-    os.cpu_count() reports, capped by OMP_NUM_THREADS where that is set (the
-    GPU box exports the CPU share of one GPU there, 16, whatever the host's
-    core count)."""
+    os.cpu_count() reports, capped by OMP_NUM_THREADS where that is set (a
+    job scheduler that shares the host between GPUs exports each job's CPU
+    share there, whatever the host's core count)."""
     count = os.cpu_count() or 1
     env = os.environ.get("OMP_NUM_THREADS")
     threads = min(count, int(env)) if env and env.isdigit() and int(env) > 0 else count
