@@ -46,15 +46,19 @@ def _protected(n, spec):
     return mask
 
 
-def _run_and_check(spec, hip_device, *, check_layers=None, score_aggregation="mean", layer_aggregation="mean"):
+def _run_and_check(spec, hip_device, *, check_layers=None, score_aggregation="mean", layer_aggregation="mean",
+                   compaction_order="auto"):
     from kvcompress_mi355x import workloads
 
     host = workloads.build_synthetic_cache(spec, "cpu", seed=0)
     cache = workloads.move_cache(host, hip_device)
     pipeline, batch = workloads.build_pipeline(
-        cache, score_aggregation=score_aggregation, layer_aggregation=layer_aggregation
+        cache, score_aggregation=score_aggregation, layer_aggregation=layer_aggregation,
+        compaction_order=compaction_order,
     )
     keep, tables, freed = pipeline.step(batch)
+    if compaction_order != "auto":
+        assert pipeline.compaction_form.chosen == compaction_order
     torch.cuda.synchronize()
     offs = [0]
     for n in spec.seq_lens:
@@ -187,6 +191,18 @@ def test_fp16_decode_shape(hip_device) -> None:
 
     spec = workloads.config_spec(5, n_layers=2, score_layer_stride=1, seq_lens=(4300, 7000, 4224))
     _run_and_check(spec, hip_device)
+
+
+@pytest.mark.parametrize("order", ["layer_major", "interleaved"])
+def test_pinned_compaction_order(hip_device, order) -> None:
+    """A pipeline whose compaction layer order is pinned runs no trials and
+    compacts every layer bit-exactly in that order (private and in place)."""
+    from kvcompress_mi355x import workloads
+
+    spec = workloads.config_spec(2, n_layers=4, score_layer_stride=2, seq_lens=(4224, 6000), budget=2048, max_model_len=16384)
+    _run_and_check(spec, hip_device, compaction_order=order)
+    spec = workloads.config_spec(4, n_layers=2, score_layer_stride=1, seq_lens=(12000, 7000), pool_pages=200, max_model_len=32768)
+    _run_and_check(spec, hip_device, compaction_order=order)
 
 
 SHARED_BUFFER_CASES = [

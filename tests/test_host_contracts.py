@@ -135,6 +135,26 @@ def test_registry_creates_and_rejects() -> None:
         registry.create("renamed", {}, SimpleNamespace(), _shape())
 
 
+def test_registry_names_and_origins() -> None:
+    from kvcompress_mi355x.methods.registry import canonical_method_name
+
+    registry = MethodRegistry()
+    registry.register("  Test_Method ", lambda o, c, s: _Method())
+    registry.register("other-method", lambda o, c, s: _Method(), origin="entry point pkg.mod:factory")
+    assert registry.names() == ("other-method", "test_method")
+    assert registry.origin("TEST_METHOD") == "in-process"
+    assert registry.origin("other-method") == "entry point pkg.mod:factory"
+    assert canonical_method_name("Tri-Attention_2") == "tri-attention_2"
+    for bad in ("", "  ", None, 3):
+        with pytest.raises(ValueError, match="non-empty string"):
+            canonical_method_name(bad)
+    for bad in ("-", "_-", "tri attention", "tri.attention"):
+        with pytest.raises(ValueError, match="only letters, digits"):
+            canonical_method_name(bad)
+    with pytest.raises(TypeError, match="must be callable"):
+        registry.register("not_callable", 5)  # type: ignore[arg-type]
+
+
 def test_builtin_method_registered_and_api_version() -> None:
     import kvcompress_mi355x
 
