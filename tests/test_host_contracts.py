@@ -162,6 +162,18 @@ def test_builtin_method_registered_and_api_version() -> None:
     assert kvcompress_mi355x.METHOD_API_VERSION == 1
 
 
+def test_scoring_layer_sample_kats() -> None:
+    """The reference's layer-sample cases (tests/test_selection.py:283-366):
+    five layers at stride 2 score layers 0, 2, 4; six layers score the same
+    three (the last layer is not added)."""
+    assert tri_method.scoring_layer_indices(5, 2) == (0, 2, 4)
+    assert tri_method.scoring_layer_indices(6, 2) == (0, 2, 4)
+    assert tri_method.scoring_layer_indices(48, 8) == (0, 8, 16, 24, 32, 40)
+    assert tri_method.scoring_layer_indices(3, 1) == (0, 1, 2)
+    with pytest.raises(ValueError):
+        tri_method.scoring_layer_indices(4, 0)
+
+
 def test_mtp_layer_names_and_gqa_width() -> None:
     assert tri_method.is_mtp_cache_layer("mtp.layers.0.self_attn.attn")
     assert tri_method.is_mtp_cache_layer("draft_model.mtp.layers.1.self_attn.attn")

@@ -47,6 +47,15 @@ def queries_per_kv_head(model_shape: ModelShape) -> int:
     return model_shape.num_attention_heads // model_shape.num_kv_heads
 
 
+def scoring_layer_indices(n_layers: int, stride: int) -> tuple[int, ...]:
+    """The layers whose keys are scored: every ``stride``-th attention layer
+    from the first, and no other (tri/method.py:188,312 sample
+    ``layer_caches[::score_layer_stride]``; the last layer is not added)."""
+    if stride <= 0:
+        raise ValueError("method option 'score_layer_stride' must be positive")
+    return tuple(range(0, n_layers, stride))
+
+
 COMPACTION_ORDER_ENV = "KVCOMPRESS_MI355X_COMPACTION_ORDER"
 
 
@@ -174,7 +183,7 @@ class TriAttentionMethod(KVCompressionMethod):
                 f"expected {local_kv_heads}, got {cache.shape[2]}"
             )
         queries_per_kv_head(self.model_shape)
-        scoring = self.layer_caches[:: self.config.score_layer_stride]
+        scoring = [self.layer_caches[i] for i in scoring_layer_indices(len(self.layer_caches), self.config.score_layer_stride)]
         tables = ScoringTables.from_layer_stats([layer.stats for layer in scoring], self.offsets)
         self.pipeline = CompressionPipeline(
             scoring_k_caches=[layer.k_cache for layer in scoring],
