@@ -350,19 +350,7 @@ def test_compaction_order_choice_and_forced_order(hip_device, order) -> None:
     assert chosen in ("layer_major", "interleaved")
     assert set(pipeline.compaction_form.per_row_ms) == {"layer_major", "interleaved"}
 
-    import kvcompress_mi355x.methods.triattention.pipeline as pl
-
-    original = pl.CompactionFormChoice.__init__
-
-    def forced(self, *args, **kwargs):
-        original(self, *args, **kwargs)
-        self.chosen = order
-
-    pl.CompactionFormChoice.__init__ = forced
-    try:
-        _run_and_check(spec, hip_device)
-    finally:
-        pl.CompactionFormChoice.__init__ = original
+    _run_and_check(spec, hip_device, compaction_order=order)
 
     ispec = workloads.config_spec(4, n_layers=2, score_layer_stride=1, seq_lens=(6000,), pool_pages=60, max_model_len=16384)
     icache = workloads.move_cache(workloads.build_synthetic_cache(ispec, "cpu", seed=2), hip_device)
