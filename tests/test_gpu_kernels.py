@@ -717,6 +717,76 @@ def test_compact_bit_exact(hip_device, mode: str, pattern: str, path: str) -> No
         assert freed[b].cpu().tolist() == want_freed
 
 
+@pytest.mark.parametrize("mode", ["private", "inplace"])
+def test_compact_layer_extent_past_32_bit_offsets(hip_device, mode: str) -> None:
+    """A layer pool of 16400 pages of 256 KB (4.30 GB each for K and V): the
+    layer-major planned copy stores through 32-bit buffer offsets only for
+    pools below 4 GiB, so this one takes the global stores.  The sequences'
+    pages sit at the end of the pool, half of them past byte 2^32, and every
+    row lands bit-exact against the oracle run on those pages alone."""
+    _, _, cache = _kvc()
+    from kvcompress_mi355x.methods.triattention import _device as dev
+
+    kv, dim, budget = 8, 128, 512
+    page_bytes = 128 * kv * dim * 2
+    pool = (1 << 32) // page_bytes + 16
+    assert pool * page_bytes > (1 << 32)
+    g = torch.Generator().manual_seed(11)
+    lens = [1000, 700]
+    far = list(range(pool - 24, pool))  # pages 16376 .. 16399; 16384 starts at byte 2^32
+    order = [far[i] for i in torch.randperm(len(far), generator=g).tolist()]
+    src_tables, dst_tables, cur = [], [], 0
+    for n in lens:
+        nb = -(-n // 128)
+        src_tables.append(order[cur : cur + nb])
+        cur += nb
+    if mode == "private":
+        for _ in lens:
+            dst_tables.append(order[cur : cur + budget // 128])
+            cur += budget // 128
+    keeps = [torch.sort(torch.randperm(n, generator=g)[:budget]).values for n in lens]
+    used = sorted({p for t in src_tables + dst_tables for p in t})
+    # Only the pages the sequences use are filled; the rest is never read.
+    k = torch.empty((pool, 128, kv, dim), dtype=torch.bfloat16, device=hip_device)
+    v = torch.empty_like(k)
+    mini_k = torch.randn(len(used), 128, kv, dim, generator=g).to(torch.bfloat16)
+    mini_v = torch.randn(len(used), 128, kv, dim, generator=g).to(torch.bfloat16)
+    idx = torch.tensor(used, dtype=torch.int64, device=hip_device)
+    k.index_copy_(0, idx, mini_k.to(hip_device))
+    v.index_copy_(0, idx, mini_v.to(hip_device))
+    # Oracle over the used pages, renumbered 0 .. len(used) - 1.
+    remap = {p: i for i, p in enumerate(used)}
+    for b in range(len(lens)):
+        dst = dst_tables[b] if mode == "private" else src_tables[b][: -(-budget // 128)]
+        ref.method_compress([mini_k], [mini_v], torch.tensor([remap[p] for p in src_tables[b]]),
+                            torch.tensor([remap[p] for p in dst]), keeps[b], budget)
+    so, si, _ = dev.ragged(src_tables, hip_device)
+    do = di = None
+    if mode == "private":
+        do, di, _ = dev.ragged(dst_tables, hip_device)
+    cache.compact_layers(
+        dev.pointer_table([k], hip_device),
+        dev.pointer_table([v], hip_device),
+        num_pages=pool,
+        page_stride=int(k.stride(0)),
+        row_elems=kv * dim,
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=hip_device),
+        src_block_offsets=so,
+        src_block_ids=si,
+        dst_block_offsets=do,
+        dst_block_ids=di,
+        keep=torch.stack(keeps).to(hip_device),
+        budget=budget,
+        workspace=torch.empty((cache.compact_workspace_bytes(len(lens), budget),), dtype=torch.uint8, device=hip_device),
+        layer_order="layer_major",
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(k.index_select(0, idx).cpu(), mini_k)
+    assert torch.equal(v.index_select(0, idx).cpu(), mini_v)
+    del k, v
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("kv,dim", [(1, 128), (4, 128), (8, 128), (10, 128)], ids=["256B", "1KB", "2KB", "2560B"])
 def test_compact_planned_row_widths(hip_device, kv: int, dim: int) -> None:
     """The planned private form (both layer orders) for row widths that give

@@ -113,7 +113,7 @@ class DescriptorCache:
     descriptor used on a stream other than the one it was allocated on is
     recorded on that stream, so that evicting it cannot hand its memory to a
     new allocation while a kernel queued there still reads it.  ``make``,
-    ``capturing`` and ``stream_of`` are injectable for host-only tests."""
+    ``capturing`` and ``current_stream`` are injectable for host-only tests."""
 
     def __init__(self, maxsize: int = 256, *, make=None, capturing=None, current_stream=None) -> None:
         self.maxsize = int(maxsize)
